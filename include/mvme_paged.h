@@ -1,0 +1,174 @@
+/*
+ * mvme_paged.h -- C ABI of the MI355X (gfx950) paged-attention library.
+ *
+ * One shared object, libmvme_paged.so, holds every hand-written HIP kernel of
+ * the paged KV-cache hot path: the KV scatter (slot mapping, decode-batch and
+ * contiguous-range variants), the block-table gather, GQA decode attention
+ * with a split-K merge, and ragged chunked paged prefill on bf16/fp16 MFMA.
+ *
+ * Conventions shared by every entry point:
+ *   - All pointers are device pointers except where noted.  Tensors are
+ *     contiguous row-major; the KV cache of one layer is
+ *     [num_blocks, block_size, kv_heads, head_dim].
+ *   - Metadata (tables, lengths, slots, offsets) is int64, matching the
+ *     reference's contract.
+ *   - `stream` is a hipStream_t passed as void* (0 = the null stream).
+ *     Every kernel is launched on that stream; no entry point allocates,
+ *     frees, synchronises or copies to the host, so calls are legal inside
+ *     HIP graph capture.
+ *   - Return value: MVME_OK, or an error code with a message readable through
+ *     mvme_last_error() (thread-local, valid until the next failing call on
+ *     the same thread).  Argument errors are detected before any launch.
+ *   - Metadata *values* are not trusted blindly: out-of-range page ids and
+ *     slots are treated as absent (skipped rows, -inf scores, zero output),
+ *     never dereferenced.
+ */
+#ifndef MVME_PAGED_H
+#define MVME_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MVME_ABI_VERSION 1
+
+/* Element types of the KV cache, queries and outputs. */
+enum mvme_dtype { MVME_FP16 = 0, MVME_BF16 = 1 };
+
+/* Status codes. */
+enum mvme_status { MVME_OK = 0, MVME_EINVAL = 1, MVME_ELAUNCH = 2, MVME_EWORKSPACE = 3 };
+
+/* ABI version of the loaded library (MVME_ABI_VERSION at build time). */
+int mvme_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* mvme_last_error(void);
+
+/*
+ * KV scatter through a slot mapping: for every t < tokens with
+ * 0 <= slot_mapping[t] < num_blocks*block_size,
+ *   key_cache row slot_mapping[t]   <- key row t
+ *   value_cache row slot_mapping[t] <- value row t
+ * where a row is kv_heads*head_dim elements.  Bit-exact byte copy.
+ * key/value rows are `key_token_stride` / `value_token_stride` elements apart
+ * (the [kv_heads, head_dim] part of each row must be contiguous).
+ * Replaces: write_kv_cache_slots_cuda / kv_write_slots_kernel
+ *   (mini_engine/kernels/csrc/data.cu:194-250), bound as
+ *   extension.write_kv_cache_slots (csrc/bindings.cpp:220) and called from
+ *   write_kv_cache_slots (mini_engine/kernels/data.py:84-130).
+ */
+int mvme_write_kv_cache_slots(void* key_cache, void* value_cache,
+                              int64_t num_blocks, int64_t block_size,
+                              int64_t kv_heads, int64_t head_dim,
+                              const int64_t* slot_mapping,
+                              const void* key, const void* value, int64_t tokens,
+                              int64_t key_token_stride, int64_t value_token_stride,
+                              int dtype, void* stream);
+
+/*
+ * Decode-step scatter of one token per sequence: for b < batch,
+ *   pos = token_offsets[b]; page = block_tables[b, pos / block_size];
+ *   slot = page*block_size + pos % block_size  (skipped if pos or page invalid)
+ * Replaces: write_kv_cache_batch_cuda / kv_write_batch_kernel
+ *   (mini_engine/kernels/csrc/data.cu:88-107, :175-192), bound as
+ *   extension.write_kv_cache_batch (csrc/bindings.cpp:128-150, :215) and
+ *   called from write_kv_cache_batch (mini_engine/kernels/data.py:67-81).
+ */
+int mvme_write_kv_cache_batch(void* key_cache, void* value_cache,
+                              int64_t num_blocks, int64_t block_size,
+                              int64_t kv_heads, int64_t head_dim,
+                              const int64_t* block_tables, int64_t table_width,
+                              const int64_t* token_offsets,
+                              const void* key, const void* value, int64_t batch,
+                              int dtype, void* stream);
+
+/*
+ * Contiguous-range write of one sequence: token t < tokens goes to logical
+ * position token_offset + t through block_ids[num_ids].
+ * Replaces: write_kv_cache_cuda / kv_write_kernel
+ *   (mini_engine/kernels/csrc/data.cu:67-86, :165-173), bound as
+ *   extension.write_kv_cache (csrc/bindings.cpp:98-126, :214) and called from
+ *   write_kv_cache (mini_engine/kernels/data.py:39-64) and
+ *   KVCachePool.write_cuda (mini_engine/cache/kv_cache.py:123-145).
+ */
+int mvme_write_kv_cache(void* key_cache, void* value_cache,
+                        int64_t num_blocks, int64_t block_size,
+                        int64_t kv_heads, int64_t head_dim,
+                        const int64_t* block_ids, int64_t num_ids, int64_t token_offset,
+                        const void* key, const void* value, int64_t tokens,
+                        int dtype, void* stream);
+
+/*
+ * Block-table gather of the logical prefix [0, token_count) of one sequence
+ * into dense [token_count, kv_heads, head_dim] outputs (rows whose page id is
+ * out of range are zero-filled).  Bit-exact.
+ * Replaces: KVCachePool.gather (mini_engine/cache/kv_cache.py:147-166), which
+ * the reference implements with torch advanced indexing.
+ */
+int mvme_gather_kv_cache(void* key_out, void* value_out,
+                         const void* key_cache, const void* value_cache,
+                         int64_t num_blocks, int64_t block_size,
+                         int64_t kv_heads, int64_t head_dim,
+                         const int64_t* block_ids, int64_t num_ids, int64_t token_count,
+                         int dtype, void* stream);
+
+/*
+ * Bytes of device workspace mvme_paged_attention needs for these shapes
+ * (0 when no split-K merge is required).  Pure host function.
+ * partition_tokens: 0 selects the library's default partition size.
+ */
+size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                           int64_t head_dim, int64_t block_size,
+                                           int64_t table_width, int64_t partition_tokens);
+
+/*
+ * GQA decode attention over block tables (one query token per sequence):
+ *   out[b, h, :] = softmax(q[b,h,:] . K_b^T / sqrt(head_dim)) V_b
+ * where K_b/V_b are the first context_lens[b] tokens of sequence b addressed
+ * through block_tables[b, :] and kv head h / (q_heads / kv_heads).
+ * Sequences with context_lens[b] <= 0 or beyond the table capacity produce
+ * zeros; out-of-range pages are skipped.  fp32 accumulation, fp32 split-K
+ * merge.  `workspace` must hold mvme_paged_attention_workspace_size(...)
+ * bytes (may be NULL when that is 0).
+ * Replaces: paged_attention_cuda, attention_vector128, attention_partition
+ *   and merge_partitions (mini_engine/kernels/csrc/paged_attention.cu:52-280),
+ *   bound as extension.paged_attention (csrc/bindings.cpp:152-184, :196-199)
+ *   and called from paged_attention (mini_engine/kernels/paged.py:8-22).
+ */
+int mvme_paged_attention(void* out, const void* query,
+                         const void* key_cache, const void* value_cache,
+                         const int64_t* block_tables, const int64_t* context_lens,
+                         int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                         int64_t num_blocks, int64_t block_size, int64_t table_width,
+                         int64_t partition_tokens, int dtype,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Ragged chunked paged prefill: packed queries q[total_tokens, q_heads,
+ * head_dim]; sequence s owns rows [cu_seqlens_q[s], cu_seqlens_q[s+1]), whose
+ * i-th row sits at absolute position query_starts[s] + i and attends keys
+ * [0, query_starts[s] + i] of that sequence through block_tables[s, :]
+ * (causal inside the chunk).  context_lens[s] = query_starts[s] + rows(s).
+ * Rows whose position is inconsistent with the metadata produce zeros.
+ * Replaces: paged_prefill_attention_cuda / paged_prefill_kernel
+ *   (mini_engine/kernels/csrc/prefill.cu:106-240), bound as
+ *   extension.paged_prefill_attention (csrc/bindings.cpp:219) and called from
+ *   paged_prefill_attention (mini_engine/kernels/prefill.py:61-131).
+ */
+int mvme_paged_prefill_attention(void* out, const void* q,
+                                 const void* key_cache, const void* value_cache,
+                                 const int64_t* cu_seqlens_q, const int64_t* query_starts,
+                                 const int64_t* block_tables, const int64_t* context_lens,
+                                 int64_t num_seqs, int64_t total_tokens,
+                                 int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                 int64_t num_blocks, int64_t block_size, int64_t table_width,
+                                 int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MVME_PAGED_H */

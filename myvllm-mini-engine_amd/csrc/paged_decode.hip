@@ -1,0 +1,449 @@
+// GQA paged decode attention for gfx950.
+//
+// Work decomposition: one work-group (4 waves, 256 lanes) per
+// (sequence, kv head, G-query-head tile, partition of `partition` tokens).
+// All G query heads that share a kv head are served by the same loads, so
+// every K/V byte of a partition is fetched from HBM exactly once.
+//
+// Lane layout inside a wave: a token row of one kv head is head_dim*2 bytes
+// = D/8 16-byte chunks; LPT (next power of two >= D/8) consecutive lanes
+// cover one token, so one global_load_dwordx4 per lane moves 64/LPT whole
+// token rows (1 KiB for D=128: four 256-byte rows).  Each wave issues four
+// K loads and four V loads per iteration before touching any of them.
+//
+// Scores: packed dot2 (fp16/bf16 products, fp32 accumulation) on the lane's
+// 8 elements, then a DPP reduction across the LPT lanes of the token.
+// Softmax: online, fp32, base-2 exponent with log2(e)/sqrt(D) folded into
+// the scale.  Each token group of lanes keeps its own running max/sum/acc;
+// groups, then waves (through LDS), are merged at the end.
+// Split-K: partitions > 1 write fp32 (acc, max, sum) partials and a merge
+// kernel combines them; sequences that fit one partition write the output
+// directly from the attention kernel.
+#include "mvme_common.h"
+
+namespace mvme {
+namespace {
+
+constexpr int kDecodeWaves = 4;
+constexpr int kDecodeThreads = kDecodeWaves * kWave;
+constexpr int kDecodeLoads = 4;  // K (and V) loads per lane per iteration
+
+template <int D>
+struct DecodeShape {
+    static constexpr int kChunks = D / 8;  // 16-byte chunks per token row
+    static constexpr int kLpt = kChunks <= 1 ? 1 : kChunks <= 2 ? 2 : kChunks <= 4 ? 4
+                              : kChunks <= 8 ? 8 : kChunks <= 16 ? 16 : kChunks <= 32 ? 32 : 64;
+    static constexpr int kTpl = kWave / kLpt;          // tokens per load
+    static constexpr int kTpi = kTpl * kDecodeLoads;   // tokens per wave iteration
+    static constexpr int kStep = kTpi * kDecodeWaves;  // tokens per work-group iteration
+};
+
+struct DecodeArgs {
+    void* out;
+    const void* query;
+    const void* key_cache;
+    const void* value_cache;
+    const int64_t* tables;
+    const int64_t* lens;
+    float* ws_acc;  // [batch*q_heads, max_parts, D]
+    float* ws_ml;   // [batch*q_heads, max_parts, 2]  (max in log2 units, sum)
+    int q_heads;
+    int kv_heads;
+    int group;      // q_heads / kv_heads
+    int gtiles;     // group / G
+    int64_t num_blocks;
+    int block_size;
+    int table_width;
+    int capacity;   // table_width * block_size
+    int partition;  // tokens per partition (multiple of DecodeShape::kStep)
+    int max_parts;
+    float scale_log2;
+};
+
+// Number of partitions a sequence of context length `len64` occupies; 0
+// tokens still owns partition 0 so that its (zero) output gets written.
+__device__ inline int seq_tokens(int64_t len64, int capacity) {
+    return (len64 > 0 && len64 <= capacity) ? (int)len64 : 0;
+}
+
+template <typename T, int D, int G, bool PAGE_UNIFORM>
+__global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs a) {
+    using S = DecodeShape<D>;
+    constexpr int L = kDecodeLoads;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = threadIdx.x / kWave;
+    const int tl = lane / S::kLpt;  // token slot inside one load
+    const int c = lane % S::kLpt;   // 16-byte chunk of the token row
+    const bool chunk_ok = c < S::kChunks;
+
+    const int unit = blockIdx.x;
+    const int part = blockIdx.y;
+    const int per_seq = a.kv_heads * a.gtiles;
+    const int b = unit / per_seq;
+    const int r = unit - b * per_seq;
+    const int kvh = r / a.gtiles;
+    const int h0 = kvh * a.group + (r - kvh * a.gtiles) * G;
+
+    const int len = seq_tokens(a.lens[b], a.capacity);
+    const int nparts = len > 0 ? (len + a.partition - 1) / a.partition : 1;
+    if (part >= nparts) return;
+    const int start = part * a.partition;
+    const int end = min(start + a.partition, len);
+
+    // Query slice of this lane for every head of the tile (8 elements each).
+    uint32_t q[G][4];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        u32x4 w = {0u, 0u, 0u, 0u};
+        if (chunk_ok)
+            w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.query) +
+                                                ((int64_t)b * a.q_heads + h0 + g) * D + 8 * c);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[g][i] = w[i];
+    }
+
+    float m[G], l[G], acc[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = kNegInf;
+        l[g] = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = 0.f;
+    }
+
+    const int64_t row_elems = (int64_t)a.kv_heads * D;
+    const int64_t page_elems = (int64_t)a.block_size * row_elems;
+    const uint16_t* kbase = static_cast<const uint16_t*>(a.key_cache) + kvh * D + 8 * c;
+    const uint16_t* vbase = static_cast<const uint16_t*>(a.value_cache) + kvh * D + 8 * c;
+    const int64_t* table = a.tables + (int64_t)b * a.table_width;
+
+    for (int it = start + wave * S::kTpi; it < end; it += S::kStep) {
+        u32x4 kk[L], vv[L];
+        bool ok[L];
+        if constexpr (PAGE_UNIFORM) {
+            // The whole iteration lies inside one page: one scalar lookup.
+            const int64_t page = table[it / a.block_size];
+            const bool page_ok = page >= 0 && page < a.num_blocks;
+            const int64_t base = page * page_elems + (int64_t)(it % a.block_size) * row_elems;
+#pragma unroll
+            for (int u = 0; u < L; ++u) {
+                const int slot = u * S::kTpl + tl;
+                ok[u] = page_ok && it + slot < end;
+                const int64_t off = base + slot * row_elems;
+                kk[u] = vv[u] = u32x4{0u, 0u, 0u, 0u};
+                if (ok[u] && chunk_ok) {
+                    kk[u] = *reinterpret_cast<const u32x4*>(kbase + off);
+                    vv[u] = *reinterpret_cast<const u32x4*>(vbase + off);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < L; ++u) {
+                const int t = it + u * S::kTpl + tl;
+                int64_t page = -1;
+                if (t < end) page = table[t / a.block_size];
+                ok[u] = page >= 0 && page < a.num_blocks;
+                const int64_t off = page * page_elems + (int64_t)(t % a.block_size) * row_elems;
+                kk[u] = vv[u] = u32x4{0u, 0u, 0u, 0u};
+                if (ok[u] && chunk_ok) {
+                    kk[u] = *reinterpret_cast<const u32x4*>(kbase + off);
+                    vv[u] = *reinterpret_cast<const u32x4*>(vbase + off);
+                }
+            }
+        }
+
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float s[L];
+#pragma unroll
+            for (int u = 0; u < L; ++u) {
+                float d = 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) d = T::dot2(kk[u][i], q[g][i], d);
+                d = group_sum<S::kLpt>(d) * a.scale_log2;
+                s[u] = ok[u] ? d : kNegInf;
+            }
+            float mx = s[0];
+#pragma unroll
+            for (int u = 1; u < L; ++u) mx = fmaxf(mx, s[u]);
+            const float mn = fmaxf(m[g], mx);
+            const float ref = mn == kNegInf ? 0.f : mn;
+            const float alpha = fast_exp2(m[g] - ref);
+            float p[L];
+            float psum = 0.f;
+#pragma unroll
+            for (int u = 0; u < L; ++u) {
+                p[u] = fast_exp2(s[u] - ref);
+                psum += p[u];
+            }
+            l[g] = l[g] * alpha + psum;
+            m[g] = mn;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[g][i] *= alpha;
+#pragma unroll
+            for (int u = 0; u < L; ++u) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[g][2 * i] = fmaf(p[u], T::lo(vv[u][i]), acc[g][2 * i]);
+                    acc[g][2 * i + 1] = fmaf(p[u], T::hi(vv[u][i]), acc[g][2 * i + 1]);
+                }
+            }
+        }
+    }
+
+    // Merge the token groups of this wave (lanes with equal chunk index).
+#pragma unroll
+    for (int mask = S::kLpt; mask < kWave; mask <<= 1) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float mo = shfl_xor(m[g], mask);
+            const float lo = shfl_xor(l[g], mask);
+            const float mn = fmaxf(m[g], mo);
+            const float ref = mn == kNegInf ? 0.f : mn;
+            const float a1 = fast_exp2(m[g] - ref);
+            const float a2 = fast_exp2(mo - ref);
+            l[g] = l[g] * a1 + lo * a2;
+            m[g] = mn;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float ao = shfl_xor(acc[g][i], mask);
+                acc[g][i] = acc[g][i] * a1 + ao * a2;
+            }
+        }
+    }
+
+    // Merge the waves through LDS.
+    __shared__ float sm_acc[kDecodeWaves][G][D];
+    __shared__ float sm_ml[kDecodeWaves][G][2];
+    if (tl == 0 && chunk_ok) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) sm_acc[wave][g][8 * c + i] = acc[g][i];
+            if (c == 0) {
+                sm_ml[wave][g][0] = m[g];
+                sm_ml[wave][g][1] = l[g];
+            }
+        }
+    }
+    __syncthreads();
+
+    for (int idx = threadIdx.x; idx < G * D; idx += kDecodeThreads) {
+        const int g = idx / D;
+        const int d = idx - g * D;
+        float mx = sm_ml[0][g][0];
+#pragma unroll
+        for (int w = 1; w < kDecodeWaves; ++w) mx = fmaxf(mx, sm_ml[w][g][0]);
+        const float ref = mx == kNegInf ? 0.f : mx;
+        float sum = 0.f, o = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDecodeWaves; ++w) {
+            const float f = fast_exp2(sm_ml[w][g][0] - ref);
+            sum += sm_ml[w][g][1] * f;
+            o += sm_acc[w][g][d] * f;
+        }
+        const int64_t bh = (int64_t)b * a.q_heads + h0 + g;
+        if (nparts == 1) {
+            static_cast<uint16_t*>(a.out)[bh * D + d] = T::from_float(sum > 0.f ? o / sum : 0.f);
+        } else {
+            const int64_t row = bh * a.max_parts + part;
+            a.ws_acc[row * D + d] = o;
+            if (d == 0) {
+                a.ws_ml[row * 2] = mx;
+                a.ws_ml[row * 2 + 1] = sum;
+            }
+        }
+    }
+}
+
+// Split-K combine: out = sum_p acc_p 2^(m_p - M) / sum_p l_p 2^(m_p - M).
+// Partitions that never saw a valid token carry m = -inf and contribute 0;
+// an all-empty sequence produces 0.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
+    const int64_t bh = blockIdx.x;
+    const int b = (int)(bh / a.q_heads);
+    const int len = seq_tokens(a.lens[b], a.capacity);
+    const int nparts = len > 0 ? (len + a.partition - 1) / a.partition : 1;
+    if (nparts == 1) return;  // written directly by the attention kernel
+    const float* ml = a.ws_ml + bh * a.max_parts * 2;
+    const float* acc = a.ws_acc + bh * a.max_parts * D;
+    float mx = kNegInf;
+    for (int p = 0; p < nparts; ++p) mx = fmaxf(mx, ml[2 * p]);
+    const float ref = mx == kNegInf ? 0.f : mx;
+    float sum = 0.f;
+    for (int p = 0; p < nparts; ++p) sum += ml[2 * p + 1] * fast_exp2(ml[2 * p] - ref);
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        float o = 0.f;
+        for (int p = 0; p < nparts; ++p) o += acc[(int64_t)p * D + d] * fast_exp2(ml[2 * p] - ref);
+        static_cast<uint16_t*>(a.out)[bh * D + d] = T::from_float(sum > 0.f ? o / sum : 0.f);
+    }
+}
+
+struct DecodePlan {
+    int partition;
+    int max_parts;
+    int gtile;  // G of the kernel instance
+    int step;
+};
+
+int decode_step_tokens(int64_t head_dim) {
+    switch (head_dim) {
+        case 16: return DecodeShape<16>::kStep;
+        case 32: return DecodeShape<32>::kStep;
+        case 64: return DecodeShape<64>::kStep;
+        case 80: return DecodeShape<80>::kStep;
+        case 96: return DecodeShape<96>::kStep;
+        case 128: return DecodeShape<128>::kStep;
+        case 192: return DecodeShape<192>::kStep;
+        case 256: return DecodeShape<256>::kStep;
+        default: return 0;
+    }
+}
+
+int decode_tile_tokens(int64_t head_dim) { return decode_step_tokens(head_dim) / kDecodeWaves; }
+
+// Host-side partition choice: enough work-groups to give every CU several
+// waves (the whole table capacity counted, since lengths stay on the device)
+// while keeping partitions long enough to amortise the merge.
+DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                            int64_t block_size, int64_t table_width, int64_t requested) {
+    DecodePlan p{};
+    const int64_t group = q_heads / kv_heads;
+    p.gtile = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
+    p.step = decode_step_tokens(head_dim);
+    const int64_t cap = table_width * block_size;
+    const int64_t cap_steps = (cap + p.step - 1) / p.step * p.step;
+    int64_t part;
+    if (requested > 0) {
+        part = (requested + p.step - 1) / p.step * p.step;
+    } else {
+        const int64_t units = batch * kv_heads * (group / p.gtile);
+        constexpr int64_t kTargetGroups = 1024;  // 256 CUs x 4 work-groups
+        part = (cap * units + kTargetGroups - 1) / kTargetGroups;
+        part = (part + p.step - 1) / p.step * p.step;
+        if (part < 256) part = 256;  // short partitions only add merge traffic
+        // Small problems are launch-bound: one partition avoids the merge launch.
+        if (cap * units <= 64 * 1024) part = cap_steps;
+    }
+    if (part < p.step) part = p.step;
+    if (part > cap_steps) part = cap_steps;
+    p.partition = (int)part;
+    p.max_parts = (int)((cap + part - 1) / part);
+    return p;
+}
+
+template <typename T, int D, int G>
+void launch_decode(const DecodeArgs& a, int units, bool page_uniform, hipStream_t s) {
+    const dim3 grid(units, a.max_parts);
+    if (page_uniform)
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, true>), grid, dim3(kDecodeThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, false>), grid, dim3(kDecodeThreads), 0, s, a);
+    if (a.max_parts > 1)
+        hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(units / a.kv_heads / a.gtiles * a.q_heads),
+                           dim3(D < 256 ? D : 256), 0, s, a);
+}
+
+template <typename T, int D>
+void launch_decode_g(const DecodeArgs& a, int gtile, int units, bool page_uniform, hipStream_t s) {
+    if (gtile == 4) launch_decode<T, D, 4>(a, units, page_uniform, s);
+    else if (gtile == 2) launch_decode<T, D, 2>(a, units, page_uniform, s);
+    else launch_decode<T, D, 1>(a, units, page_uniform, s);
+}
+
+template <typename T>
+void launch_decode_d(const DecodeArgs& a, int64_t head_dim, int gtile, int units, bool pu, hipStream_t s) {
+    switch (head_dim) {
+        case 16: launch_decode_g<T, 16>(a, gtile, units, pu, s); break;
+        case 32: launch_decode_g<T, 32>(a, gtile, units, pu, s); break;
+        case 64: launch_decode_g<T, 64>(a, gtile, units, pu, s); break;
+        case 80: launch_decode_g<T, 80>(a, gtile, units, pu, s); break;
+        case 96: launch_decode_g<T, 96>(a, gtile, units, pu, s); break;
+        case 128: launch_decode_g<T, 128>(a, gtile, units, pu, s); break;
+        case 192: launch_decode_g<T, 192>(a, gtile, units, pu, s); break;
+        case 256: launch_decode_g<T, 256>(a, gtile, units, pu, s); break;
+    }
+}
+
+int check_decode_shapes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                        int64_t num_blocks, int64_t block_size, int64_t table_width, int dtype) {
+    if (!valid_dtype(dtype)) return fail(MVME_EINVAL, "FP16/BF16 required");
+    if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || num_blocks <= 0)
+        return fail(MVME_EINVAL, "empty batch/heads/cache");
+    if (block_size <= 0) return fail(MVME_EINVAL, "block size mismatch");
+    if (q_heads % kv_heads != 0) return fail(MVME_EINVAL, "head dimension or GQA mismatch");
+    if (decode_step_tokens(head_dim) == 0)
+        return fail(MVME_EINVAL, "supported head_dim: 16,32,64,80,96,128,192,256");
+    if (table_width <= 0) return fail(MVME_EINVAL, "invalid block table");
+    if (table_width * block_size > 1048576) return fail(MVME_EINVAL, "maximum table capacity is 1M tokens");
+    if (batch * q_heads > 2147483647) return fail(MVME_EINVAL, "batch/head product too large");
+    return MVME_OK;
+}
+
+}  // namespace
+}  // namespace mvme
+
+using namespace mvme;
+
+extern "C" size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_heads, int64_t kv_heads,
+                                                      int64_t head_dim, int64_t block_size,
+                                                      int64_t table_width, int64_t partition_tokens) {
+    if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || block_size <= 0 ||
+        table_width <= 0 || decode_step_tokens(head_dim) == 0)
+        return 0;
+    const DecodePlan p = make_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, table_width,
+                                          partition_tokens);
+    if (p.max_parts <= 1) return 0;
+    return (size_t)batch * q_heads * p.max_parts * (head_dim + 2) * sizeof(float);
+}
+
+extern "C" int mvme_paged_attention(void* out, const void* query, const void* key_cache,
+                                    const void* value_cache, const int64_t* block_tables,
+                                    const int64_t* context_lens, int64_t batch, int64_t q_heads,
+                                    int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
+                                    int64_t block_size, int64_t table_width, int64_t partition_tokens,
+                                    int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    if (int rc = check_decode_shapes(batch, q_heads, kv_heads, head_dim, num_blocks, block_size,
+                                     table_width, dtype))
+        return rc;
+    if (!out || !query || !key_cache || !value_cache || !block_tables || !context_lens)
+        return fail(MVME_EINVAL, "paged attention received a null pointer");
+    const DecodePlan p = make_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, table_width,
+                                          partition_tokens);
+    const size_t need = mvme_paged_attention_workspace_size(batch, q_heads, kv_heads, head_dim, block_size,
+                                                            table_width, partition_tokens);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(MVME_EWORKSPACE, "paged attention workspace too small: need " + std::to_string(need) +
+                                         " bytes, got " + std::to_string(workspace_bytes));
+    const int64_t group = q_heads / kv_heads;
+    const int64_t units = batch * kv_heads * (group / p.gtile);
+    if (units > 2147483647) return fail(MVME_EINVAL, "batch/head product too large");
+    DecodeArgs a{};
+    a.out = out;
+    a.query = query;
+    a.key_cache = key_cache;
+    a.value_cache = value_cache;
+    a.tables = block_tables;
+    a.lens = context_lens;
+    if (need > 0) {
+        a.ws_acc = static_cast<float*>(workspace);
+        a.ws_ml = a.ws_acc + batch * q_heads * p.max_parts * head_dim;
+    }
+    a.q_heads = (int)q_heads;
+    a.kv_heads = (int)kv_heads;
+    a.group = (int)group;
+    a.gtiles = (int)(group / p.gtile);
+    a.num_blocks = num_blocks;
+    a.block_size = (int)block_size;
+    a.table_width = (int)table_width;
+    a.capacity = (int)(table_width * block_size);
+    a.partition = p.partition;
+    a.max_parts = p.max_parts;
+    a.scale_log2 = kLog2e / sqrtf((float)head_dim);
+    const bool page_uniform = block_size % decode_tile_tokens(head_dim) == 0;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (dtype == MVME_FP16) launch_decode_d<Half>(a, head_dim, p.gtile, (int)units, page_uniform, s);
+    else launch_decode_d<BFloat16>(a, head_dim, p.gtile, (int)units, page_uniform, s);
+    return check_launch("paged attention");
+}

@@ -1,0 +1,79 @@
+"""Ragged chunked paged prefill attention, ``backend="hip"``.
+
+Same signature, metadata contract and validation messages as the
+reference's ``paged_prefill_attention`` (mini_engine/kernels/prefill.py:61-131)
+and its native op (mini_engine/kernels/csrc/prefill.cu:200-240).  Packed
+queries read the paged KV cache directly; D=128 runs on bf16/fp16 MFMA tiles,
+other head sizes (up to 1024) on a generic HIP kernel.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import hip_extension as ext
+
+MAX_HEAD_DIM = 1024
+
+
+def paged_prefill_attention(q, key_cache, value_cache, cu_seqlens_q, query_starts,
+                            block_tables, context_lens, block_size, *, backend="hip", validate=True):
+    """Packed causal queries read paged KV directly.
+
+    Q is [total_queries, query_heads, head_dim].  Each request describes a
+    suffix starting at its absolute query_start; context_len equals
+    start + query_count.  Validation of metadata values synchronizes the
+    device; trusted model batches can skip it.
+    """
+    if backend != "hip":
+        raise ValueError("paged prefill backend must be hip")
+    if (type(block_size) is not int or block_size <= 0 or key_cache.ndim != 4
+            or value_cache.shape != key_cache.shape or key_cache.shape[1] != block_size
+            or any(size <= 0 for size in key_cache.shape)
+            or not key_cache.is_contiguous() or not value_cache.is_contiguous()):
+        raise ValueError("paged prefill caches must be contiguous [pages, block_size, kv_heads, head_dim]")
+    if (q.ndim != 3 or q.shape[1] <= 0 or q.shape[2] != key_cache.shape[3]
+            or q.shape[1] % key_cache.shape[2]):
+        raise ValueError("paged prefill Q must be [tokens, heads, head_dim] with divisible GQA heads")
+    if q.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise ValueError("paged prefill requires FP32/FP16/BF16")
+    if key_cache.dtype != q.dtype or value_cache.dtype != q.dtype:
+        raise ValueError("paged prefill Q/K/V must share dtype")
+    metadata = (cu_seqlens_q, query_starts, block_tables, context_lens)
+    if (cu_seqlens_q.ndim != 1 or query_starts.ndim != 1 or context_lens.ndim != 1
+            or block_tables.ndim != 2 or query_starts.numel() != block_tables.shape[0]
+            or context_lens.numel() != block_tables.shape[0]
+            or cu_seqlens_q.numel() != block_tables.shape[0] + 1):
+        raise ValueError("paged prefill metadata shapes do not match request count")
+    if any(t.dtype != torch.int64 or not t.is_contiguous() for t in metadata):
+        raise ValueError("paged prefill metadata must be contiguous int64 tensors")
+    if any(t.device != q.device for t in (key_cache, value_cache, *metadata)):
+        raise ValueError("paged prefill tensors must share device")
+    if validate:
+        offsets, starts, tables, lengths = (t.tolist() for t in metadata)
+        if offsets[0] != 0 or offsets[-1] != q.shape[0] or any(b < a for a, b in zip(offsets, offsets[1:])):
+            raise ValueError("query offsets must be monotone and cover all packed queries")
+        for index, (start, length, table) in enumerate(zip(starts, lengths, tables)):
+            count = offsets[index + 1] - offsets[index]
+            if start < 0 or length != start + count or length > len(table) * block_size:
+                raise ValueError("query start/context length exceeds block table capacity or query range")
+            used = (length + block_size - 1) // block_size
+            if any(page < 0 or page >= key_cache.shape[0] for page in table[:used]):
+                raise ValueError("active block table contains an invalid physical page")
+    if q.device.type != "cuda" or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("HIP paged prefill requires HIP FP16/BF16")
+    if q.shape[2] > MAX_HEAD_DIM:
+        raise ValueError("HIP paged prefill supports head_dim up to 1024")
+    q = q.contiguous()
+    output = torch.empty_like(q)
+    if q.shape[0] == 0:
+        return output
+    lib = ext.load_hip_extension()
+    num_blocks, _, kv_heads, head_dim = key_cache.shape
+    with torch.cuda.device(q.device):
+        lib.call("mvme_paged_prefill_attention", output.data_ptr(), q.data_ptr(), key_cache.data_ptr(),
+                 value_cache.data_ptr(), cu_seqlens_q.data_ptr(), query_starts.data_ptr(),
+                 block_tables.data_ptr(), context_lens.data_ptr(), query_starts.numel(), q.shape[0],
+                 q.shape[1], kv_heads, head_dim, num_blocks, block_size, block_tables.shape[1],
+                 ext.dtype_code(q.dtype), ext.current_stream(q.device))
+    return output

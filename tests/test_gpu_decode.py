@@ -1,0 +1,180 @@
+"""GPU parity of HIP paged decode attention against the CPU oracle.
+
+Restates the reference's kernel tests (tests/test_cuda_paged_attention.py)
+for backend="hip": all supported head dims and both dtypes vs the fp32
+oracle, block/partition boundaries, metadata rejection, non-default stream,
+trusted-mode corrupt tables, graph capture with mutated inputs, and the
+benchmark workloads.  Tolerances: the north-star gate (max abs error
+<= 2e-3 fp16, <= 1.6e-2 bf16 vs the fp32 oracle) unless a tighter reference
+tolerance applies.
+"""
+
+import pytest
+import torch
+
+from gpu_cases import decode_inputs
+from mini_engine_hip.kernels.paged import paged_attention
+from oracle import c_oracle, paged_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GATE = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+
+
+def to_dev(args):
+    return [a.to(DEV) if isinstance(a, torch.Tensor) else a for a in args]
+
+
+def oracle(args):
+    q, k, v, t, l, bs = args
+    return paged_oracle.fp32_oracle(dict(zip(paged_oracle.TENSOR_NAMES, (q, k, v, t, l))), bs)
+
+
+def max_err(actual, expected):
+    return (actual.float().cpu() - expected.float()).abs().max().item()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim", [16, 32, 64, 80, 96, 128, 192, 256])
+def test_hip_gqa_splitkv_matches_oracle(dtype, dim):
+    args = decode_inputs(dtype, head_dim=dim)
+    actual = paged_attention(*to_dev(args), backend="hip")
+    expected = oracle(args)
+    assert max_err(actual, expected) <= GATE[dtype]
+    # Reference tolerance against fp32 SDPA (test_cuda_paged_attention.py:43-44).
+    atol = 0.004 if dtype == torch.bfloat16 else 0.0006
+    torch.testing.assert_close(actual.float().cpu(), expected, atol=atol, rtol=0.015)
+
+
+@pytest.mark.parametrize("block_size,lengths,heads,kv_heads", [
+    (4, (1,), 4, 4), (16, (256, 255), 8, 1),
+    (32, (257, 1025, 9), 16, 8), (16, (4097,), 16, 8),
+    (1, (3, 70), 6, 2), (7, (50, 13, 1), 12, 4), (256, (2048, 1, 700), 16, 8),
+])
+def test_hip_block_and_partition_boundaries(block_size, lengths, heads, kv_heads):
+    args = decode_inputs(torch.bfloat16, block_size=block_size, lengths=lengths, heads=heads, kv_heads=kv_heads)
+    actual = paged_attention(*to_dev(args), backend="hip")
+    assert max_err(actual, oracle(args)) <= GATE[torch.bfloat16]
+
+
+@pytest.mark.parametrize("partition", [64, 128, 256, 512, 4096])
+def test_split_count_does_not_change_result(partition):
+    """Split-K invariant: any partition size gives the single-partition answer."""
+    args = decode_inputs(torch.float16, lengths=(1, 63, 64, 65, 700, 2049), block_size=16)
+    dev = to_dev(args)
+    single = paged_attention(*dev, backend="hip", partition_tokens=1 << 20)
+    split = paged_attention(*dev, backend="hip", partition_tokens=partition)
+    assert (split.float() - single.float()).abs().max().item() <= 2e-3
+    assert max_err(split, oracle(args)) <= GATE[torch.float16]
+
+
+def test_hip_rejects_bad_metadata_and_noncontiguous_query():
+    args = to_dev(decode_inputs(torch.float16))
+    args[4][0] = 0
+    with pytest.raises(RuntimeError, match="context length"):
+        paged_attention(*args, backend="hip")
+    args[4][0] = 17
+    args[3][0, 0] = -1
+    with pytest.raises(RuntimeError, match="physical block"):
+        paged_attention(*args, backend="hip")
+    args[3][0, 0] = 0
+    args[0] = args[0].transpose(0, 1).contiguous().transpose(0, 1)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        paged_attention(*args, backend="hip")
+
+
+def test_hip_current_stream_and_trusted_invalid_indices():
+    args = decode_inputs(torch.bfloat16, lengths=(65,))
+    dev = to_dev(args)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        actual = paged_attention(*dev, backend="hip", validate=False)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    assert max_err(actual, oracle(args)) <= GATE[torch.bfloat16]
+    # Trusted mode never reads through a corrupt page id: all -1 -> zeros.
+    dev[3].fill_(-1)
+    actual = paged_attention(*dev, backend="hip", validate=False)
+    assert torch.isfinite(actual).all() and not actual.any()
+    # Lengths beyond the table capacity, or <= 0, give zeros as well.
+    dev = to_dev(args)
+    dev[4].fill_(10**6)
+    assert not paged_attention(*dev, backend="hip", validate=False).any()
+
+
+def test_single_token_context_returns_first_value_row():
+    """Closed form: context length 1 -> output = v_0 (rounded to the dtype)."""
+    args = decode_inputs(torch.float16, lengths=(1, 1, 1), block_size=16)
+    q, k, v, t, l, bs = args
+    actual = paged_attention(*to_dev(args), backend="hip").cpu()
+    group = q.shape[1] // k.shape[2]
+    for b in range(q.shape[0]):
+        v0 = v[t[b, 0], 0].repeat_interleave(group, dim=0)
+        assert torch.equal(actual[b], v0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("block_size", [4, 16, 64, 256])
+def test_graph_replay_with_mutated_query_and_lengths(dtype, block_size):
+    """Capture once, mutate q and context_lens in place, replay (cuda_graph.py:244-275 pattern)."""
+    args = decode_inputs(dtype, block_size=block_size, lengths=(1, 17, 127, 256))
+    dev = to_dev(args)
+    originals = dev[1].clone(), dev[2].clone()
+    paged_attention(*dev, backend="hip", validate=False)  # warm the allocator
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = paged_attention(*dev, backend="hip", validate=False)
+    for replay in range(3):
+        dev[4].copy_(torch.tensor([256, 128, 16, 1][replay:] + [256, 128, 16, 1][:replay], device=DEV))
+        dev[0].mul_(0.75)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = paged_attention(*dev, backend="hip", validate=False)
+        expected = oracle([x.cpu() if isinstance(x, torch.Tensor) else x for x in dev])
+        assert max_err(captured, expected) <= GATE[dtype]
+        assert torch.equal(captured, eager)
+    assert torch.equal(originals[0], dev[1]) and torch.equal(originals[1], dev[2])
+
+
+def test_oracle_c_restatement_agrees_on_gpu_case():
+    """The HIP output also sits within tolerance of the float64 C oracle."""
+    args = decode_inputs(torch.bfloat16, lengths=(5, 300), block_size=32, seed=99)
+    actual = paged_attention(*to_dev(args), backend="hip")
+    expected = c_oracle.paged_decode(*args)
+    assert max_err(actual, expected) <= GATE[torch.bfloat16]
+
+
+# ---------------------------------------------------------------------------
+# Benchmark workloads (seeded as in the benchmark).
+# ---------------------------------------------------------------------------
+
+def test_c1_make_case_b1_ctx128_fp16():
+    tensors, _ = paged_oracle.make_case(1, 128)
+    args = [tensors[n] for n in paged_oracle.TENSOR_NAMES] + [256]
+    actual = paged_attention(*to_dev(args), backend="hip")
+    result = paged_oracle.validate_output(actual.cpu(), paged_oracle.fp32_oracle(tensors, 256))
+    assert result["passed"] and result["max_absolute_error"] <= 2e-3
+
+
+def test_c3_make_case_b32_ctx2048_fp16():
+    tensors, _ = paged_oracle.make_case(32, 2048)
+    args = [tensors[n] for n in paged_oracle.TENSOR_NAMES] + [256]
+    actual = paged_attention(*to_dev(args), backend="hip")
+    result = paged_oracle.validate_output(actual.cpu(), paged_oracle.fp32_oracle(tensors, 256))
+    assert result["passed"] and result["max_absolute_error"] <= 2e-3
+
+
+def test_c4_ragged_shared_prefix_bf16():
+    """Ragged lengths in [1, 4096], 16 sequences sharing one prefix's pages."""
+    from mini_engine_hip.workloads import ragged_shared_prefix_case
+
+    case = ragged_shared_prefix_case(device=DEV)
+    args = [case[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lens")] + [16]
+    actual = paged_attention(*args, backend="hip", validate=True)
+    expected = oracle([a.cpu() if isinstance(a, torch.Tensor) else a for a in args])
+    assert max_err(actual, expected) <= GATE[torch.bfloat16]
+    # Shared prefix pages really are shared: 16 tables name the same first 64 pages.
+    tables = case["block_tables"].cpu()
+    assert all(torch.equal(tables[i, :64], tables[0, :64]) for i in range(16))

@@ -1,0 +1,211 @@
+"""GPU parity of the HIP KV scatter/gather and paged prefill against the oracle.
+
+Restates the reference's GPU tests for these paths
+(tests/test_ragged_kernels.py:102-136, tests/test_data_kernels.py:40-57,
+tests/test_kv_cache.py:6-23) for backend="hip".  KV writes and gathers must
+be bit-exact; prefill outputs must sit within the north-star gate of the
+fp32 oracle (max abs 2e-3 fp16, 1.6e-2 bf16) and within the reference's own
+tolerance (test_ragged_kernels.py:120).
+"""
+
+import pytest
+import torch
+
+from gpu_cases import prefill_inputs
+from mini_engine_hip.cache.kv_cache import KVCachePool
+from mini_engine_hip.kernels.data import write_kv_cache, write_kv_cache_batch, write_kv_cache_slots
+from mini_engine_hip.kernels.prefill import paged_prefill_attention
+from mini_engine_hip import workloads
+from oracle import c_oracle, paged_oracle
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GATE = {torch.float16: 2e-3, torch.bfloat16: 1.6e-2}
+
+
+def max_err(actual, expected):
+    return (actual.float().cpu() - expected.float().cpu()).abs().max().item()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim", [16, 128])
+def test_packed_attention_and_slot_scatter_on_nondefault_stream(dtype, dim):
+    q, key, value, offsets, starts, tables, lengths = prefill_inputs(dtype, head_dim=dim)
+    slots = torch.tensor([5, 6, 7, 9, 10, 11, 28, 29], dtype=torch.int64)
+    gen = torch.Generator().manual_seed(5)
+    source_k = torch.randn(8, 2, dim, generator=gen).to(dtype)
+    source_v = torch.randn(8, 2, dim, generator=gen).to(dtype)
+    expected_k, expected_v = key.clone(), value.clone()
+    paged_oracle.write_kv_cache_slots(expected_k, expected_v, slots, source_k, source_v)
+    expected = paged_oracle.paged_prefill_attention(q, expected_k, expected_v, offsets, starts, tables,
+                                                    lengths, 4, cast=False)
+    dk, dv = key.to(DEV), value.to(DEV)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        write_kv_cache_slots(dk, dv, slots.to(DEV), source_k.to(DEV), source_v.to(DEV), backend="hip")
+        result = paged_prefill_attention(q.to(DEV), dk, dv, offsets.to(DEV), starts.to(DEV), tables.to(DEV),
+                                         lengths.to(DEV), 4, backend="hip")
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), expected_k) and torch.equal(dv.cpu(), expected_v)
+    assert max_err(result, expected) <= GATE[dtype]
+    tolerance = 0.02 if dtype == torch.bfloat16 else 0.003
+    torch.testing.assert_close(result.cpu(), expected.to(dtype), atol=tolerance, rtol=tolerance)
+
+
+def test_slot_scatter_strided_sources_and_untouched_rows():
+    """Split projection views (non-contiguous token stride) scatter bit-exactly."""
+    dtype = torch.bfloat16
+    gen = torch.Generator().manual_seed(11)
+    cache_k = torch.randn(32, 16, 8, 128, generator=gen).to(dtype)
+    cache_v = torch.randn(32, 16, 8, 128, generator=gen).to(dtype)
+    packed = torch.randn(40, 16, 128, generator=gen).to(dtype)   # [tokens, k heads | v heads, D]
+    src_k, src_v = packed[:, :8], packed[:, 8:]
+    slots = torch.randperm(32 * 16, generator=gen)[:40]
+    want_k, want_v = c_oracle.scatter_slots(cache_k, cache_v, slots, src_k, src_v)
+    dk, dv, dpacked = cache_k.to(DEV), cache_v.to(DEV), packed.to(DEV)
+    write_kv_cache_slots(dk, dv, slots.to(DEV), dpacked[:, :8], dpacked[:, 8:], backend="hip")
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), want_k) and torch.equal(dv.cpu(), want_v)
+
+
+def test_slot_scatter_trusted_out_of_range_slots_are_skipped():
+    dtype = torch.float16
+    cache_k = torch.zeros(4, 4, 2, 16, dtype=dtype, device=DEV)
+    cache_v = torch.zeros_like(cache_k)
+    slots = torch.tensor([-1, 3, 16, 1 << 40], dtype=torch.int64, device=DEV)
+    src = torch.ones(4, 2, 16, dtype=dtype, device=DEV)
+    write_kv_cache_slots(cache_k, cache_v, slots, src, src, backend="hip", validate=False)
+    torch.cuda.synchronize()
+    rows = cache_k.view(-1, 2, 16)
+    assert rows[3].eq(1).all() and rows.sum().item() == 32
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_kv_write_crosses_pages_and_uses_stream(dtype):
+    gen = torch.Generator().manual_seed(63)
+    block_size, blocks, kv_heads, dim = 4, 6, 2, 8
+    key_cache = torch.zeros(blocks, block_size, kv_heads, dim, dtype=dtype)
+    value_cache = torch.zeros_like(key_cache)
+    ids = torch.tensor([4, 1, 5], dtype=torch.long)
+    key = torch.randn(7, kv_heads, dim, generator=gen).to(dtype)
+    value = torch.randn(7, kv_heads, dim, generator=gen).to(dtype)
+    expected_k, expected_v = key_cache.clone(), value_cache.clone()
+    paged_oracle.write_kv_cache(expected_k, expected_v, ids, 1, key, value, block_size)
+    dk, dv = key_cache.to(DEV), value_cache.to(DEV)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        write_kv_cache(dk, dv, ids.to(DEV), 1, key.to(DEV), value.to(DEV), block_size, backend="hip")
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), expected_k) and torch.equal(dv.cpu(), expected_v)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_batch_write_matches_oracle(dtype):
+    gen = torch.Generator().manual_seed(64)
+    kc = torch.randn(20, 16, 8, 128, generator=gen).to(dtype)
+    vc = torch.randn(20, 16, 8, 128, generator=gen).to(dtype)
+    tables = torch.randperm(20, generator=gen)[:12].view(4, 3)
+    offsets = torch.tensor([0, 15, 16, 47], dtype=torch.int64)
+    key = torch.randn(4, 8, 128, generator=gen).to(dtype)
+    value = torch.randn(4, 8, 128, generator=gen).to(dtype)
+    want_k, want_v = kc.clone(), vc.clone()
+    paged_oracle.write_kv_cache_batch(want_k, want_v, tables, offsets, key, value, 16)
+    dk, dv = kc.to(DEV), vc.to(DEV)
+    write_kv_cache_batch(dk, dv, tables.to(DEV), offsets.to(DEV), key.to(DEV), value.to(DEV), 16, backend="hip")
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), want_k) and torch.equal(dv.cpu(), want_v)
+
+
+def test_kv_cache_pool_write_gather_and_clear():
+    """tests/test_kv_cache.py:6-23 on the HIP pool: page-crossing write, gather, clear."""
+    cache = KVCachePool(2, 3, 4, 2, 8, dtype=torch.float16, device=DEV)
+    cache.clear()
+    gen = torch.Generator().manual_seed(3)
+    key = torch.randn(3, 2, 8, generator=gen).half().to(DEV)
+    value = key + 100
+    cache.write_hip(1, [2, 0], 3, key, value)
+    got_key, got_value = cache.gather(1, [2, 0], 6)
+    assert torch.equal(got_key[3:6], key) and torch.equal(got_value[3:6], value)
+    want_k, want_v = paged_oracle.gather(cache.key[1].cpu(), cache.value[1].cpu(), [2, 0], 6)
+    assert torch.equal(got_key.cpu(), want_k) and torch.equal(got_value.cpu(), want_v)
+    assert cache.memory_bytes == 2 * 3 * 4 * 2 * 8 * 2 * 2
+    cache.key.fill_(1)
+    cache.value.fill_(1)
+    cache.clear([1])
+    assert torch.all(cache.key[:, 1] == 0) and torch.all(cache.value[:, 0] == 1)
+
+
+def test_prefill_context_beyond_dense_limit():
+    """8193-token context through 32-token pages (test_ragged_kernels.py:124-136)."""
+    block, context = 32, 8193
+    gen = torch.Generator().manual_seed(81)
+    pages = (context + block - 1) // block
+    key = torch.randn(pages, block, 1, 16, generator=gen).half()
+    value = torch.randn(pages, block, 1, 16, generator=gen).half()
+    q = torch.randn(1, 2, 16, generator=gen).half()
+    tables = torch.randperm(pages, generator=gen).view(1, -1)
+    offsets = torch.tensor([0, 1])
+    starts, lengths = torch.tensor([context - 1]), torch.tensor([context])
+    actual = paged_prefill_attention(q.to(DEV), key.to(DEV), value.to(DEV), offsets.to(DEV), starts.to(DEV),
+                                     tables.to(DEV), lengths.to(DEV), block, backend="hip")
+    expected = paged_oracle.paged_prefill_attention(q, key, value, offsets, starts, tables, lengths, block,
+                                                    cast=False)
+    assert max_err(actual, expected) <= GATE[torch.float16]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("priors,block_size", [
+    ([0, 5, 64, 300], 16), ([1000, 0, 17, 255], 256), ([3, 1, 0, 129], 4),
+])
+def test_mfma_prefill_ragged_priors(dtype, priors, block_size):
+    case = workloads.chunked_prefill_case(device=DEV, num_seqs=len(priors), new_tokens=37, block_size=block_size,
+                                          dtype=dtype, priors=priors, seed=7)
+    write_kv_cache_slots(case["key_cache"], case["value_cache"], case["slot_mapping"], case["new_key"],
+                         case["new_value"], backend="hip")
+    names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+    args = [case[n] for n in names]
+    actual = paged_prefill_attention(*args, block_size, backend="hip")
+    cpu = [a.cpu() for a in args]
+    expected = paged_oracle.paged_prefill_attention(*cpu, block_size, cast=False)
+    assert max_err(actual, expected) <= GATE[dtype]
+    # The float64 C restatement agrees too.
+    assert max_err(actual, c_oracle.paged_prefill(*cpu, block_size)) <= GATE[dtype]
+
+
+@pytest.mark.parametrize("group,heads", [(1, 8), (4, 16), (8, 16)])
+def test_mfma_prefill_gqa_groups(group, heads):
+    dtype = torch.bfloat16
+    gen = torch.Generator().manual_seed(group)
+    kv_heads = heads // group
+    block = 16
+    pages = 24
+    kc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
+    vc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
+    tables = torch.randperm(pages, generator=gen)[:20].view(2, 10)
+    cu = torch.tensor([0, 50, 71])
+    starts = torch.tensor([90, 3])
+    lens = starts + (cu[1:] - cu[:-1])
+    q = torch.randn(71, heads, 128, generator=gen).to(dtype)
+    args = [q, kc, vc, cu, starts, tables, lens]
+    actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip")
+    expected = paged_oracle.paged_prefill_attention(*args, block, cast=False)
+    assert max_err(actual, expected) <= GATE[dtype]
+
+
+def test_c5_chunked_prefill_full_size():
+    """8 sequences x 128 new tokens after U[0,3968] prior tokens, block 256, bf16."""
+    case = workloads.chunked_prefill_case(device=DEV)
+    write_kv_cache_slots(case["key_cache"], case["value_cache"], case["slot_mapping"], case["new_key"],
+                         case["new_value"], backend="hip")
+    names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+    args = [case[n] for n in names]
+    actual = paged_prefill_attention(*args, 256, backend="hip")
+    expected = paged_oracle.paged_prefill_attention(*[a.cpu() for a in args], 256, cast=False)
+    assert max_err(actual, expected) <= GATE[torch.bfloat16]
+    # Scatter bit-exactness at full size: every new row sits in its slot.
+    rows = case["key_cache"].view(-1, 8, 128)[case["slot_mapping"]]
+    assert torch.equal(rows, case["new_key"])
