@@ -1,0 +1,346 @@
+"""Benchmark of the HIP paged-attention path on one MI355X.
+
+Headline workload (one "step"): paged GQA decode, fp16, batch 32, every
+context 2048 tokens, Hq=16 / Hkv=8 / D=128, block size 256, 28 layers run
+back-to-back, each layer with its own KV pool (263 pages), own queries and
+own random non-contiguous block table (Qwen3-0.6B decode-step shapes).
+Inputs are synthetic N(0,1), resident in HBM before timing starts.
+
+Timing: a HIP graph holds the 28 layer calls; W warm-up replays, then K
+timed replays bracketed by synchronisation, HIP events on the launch stream.
+value = algorithmic HBM bytes of a step / step time (TB/s); algorithmic
+bytes count every KV row of a layer once (4096 B per token per layer) plus
+q, out, tables and lengths: 268,699,904 B per layer.
+
+Also reported (field "extra"): the other workloads of the same path --
+B=1/ctx128, B=8/ctx512 with the KV scatter, ragged B=64 with a shared
+prefix, and chunked prefill 8x128 on MFMA -- and the CPU torch path of the
+reference (restated in the oracle) timed on this host on a bounded sample.
+
+Prints ONE JSON line.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+from pathlib import Path
+import platform
+import statistics
+import subprocess
+import sys
+import time
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "myvllm-mini-engine_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "paged-decode µs/call + HBM TB/s (% peak), B=32 ctx2048 Hq16/Hkv8/D128"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+LAYERS = 28
+BATCH, CONTEXT, BLOCK = 32, 2048, 256
+HQ, HKV, D = 16, 8, 128
+BASE_SEED = 20261026
+REFERENCE_US_PER_CALL = 362.44  # RTX 5080, block 256 fp16, decode_numerical_round_20261102.json:1693
+
+
+def layer_bytes(batch=BATCH, context=CONTEXT, width=CONTEXT // BLOCK):
+    kv = batch * context * HKV * D * 2 * 2
+    return kv + 2 * batch * HQ * D * 2 + batch * width * 8 + batch * 8
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def graph_time_ms(fn, torch, *, calls_per_graph, replays, warmup):
+    """Capture `fn` (which issues calls_per_graph calls) once, time replays."""
+    fn()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / replays, graph
+
+
+def eager_wall_ms(fn, torch, repeats=5):
+    fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(repeats):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / repeats
+
+
+def max_abs(actual, expected):
+    return (actual.float().cpu() - expected.float().cpu()).abs().max().item()
+
+
+# ---------------------------------------------------------------------------
+# Headline: 28-layer decode step.
+# ---------------------------------------------------------------------------
+
+def headline(args, torch, paged_attention, workloads):
+    dev = torch.device("cuda:0")
+    layers = []
+    for layer in range(LAYERS):
+        case = workloads.decode_b32_layer(dev, seed=BASE_SEED + 2 + 1000 * layer)
+        case["out"] = torch.empty_like(case["query"])
+        layers.append(case)
+    torch.cuda.synchronize()
+    log(f"headline inputs resident: {LAYERS} layers x 2 x {layers[0]['key_cache'].numel() * 2 / 2**20:.1f} MiB")
+
+    def step():
+        for c in layers:
+            paged_attention(c["query"], c["key_cache"], c["value_cache"], c["block_tables"], c["context_lens"],
+                            BLOCK, backend="hip", validate=False, partition_tokens=args.partition,
+                            out=c["out"])
+
+    ms, graph = graph_time_ms(step, torch, calls_per_graph=LAYERS, replays=args.steps, warmup=args.warmup)
+    eager_ms = eager_wall_ms(step, torch, repeats=3)
+    return layers, ms, eager_ms
+
+
+def headline_parity(layers, oracle):
+    """Layer 0 and layer 27 against the fp32 oracle (fp16 gate 2e-3)."""
+    worst = 0.0
+    for idx in (0, LAYERS - 1):
+        c = layers[idx]
+        tensors = {"query": c["query"].cpu(), "key_cache": c["key_cache"].cpu(), "value_cache": c["value_cache"].cpu(),
+                   "block_tables": c["block_tables"].cpu(), "context_lens": c["context_lens"].cpu()}
+        ref = oracle.fp32_oracle(tensors, BLOCK)
+        worst = max(worst, max_abs(c["out"], ref))
+    return {"layers_checked": [0, LAYERS - 1], "max_abs_error": worst, "gate": 2e-3, "passed": worst <= 2e-3}
+
+
+def cpu_baseline(layers, oracle, torch, budget_s):
+    """The reference's torch decode path, restated in the oracle, on host cores."""
+    threads = torch.get_num_threads()
+    c = layers[0]
+    tensors = [c["query"].cpu(), c["key_cache"].cpu(), c["value_cache"].cpu(), c["block_tables"].cpu(),
+               c["context_lens"].cpu()]
+    oracle.paged_attention(*tensors, BLOCK)  # warm-up
+    samples = []
+    t_start = time.perf_counter()
+    while len(samples) < 5 or (time.perf_counter() - t_start < budget_s and len(samples) < 20):
+        t0 = time.perf_counter()
+        oracle.paged_attention(*tensors, BLOCK)
+        samples.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > 3 * budget_s:
+            break
+    sec = statistics.median(samples)
+    cpu_model = platform.processor() or ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                cpu_model = line.split(":", 1)[1].strip()
+    except Exception:
+        pass
+    return {"value": layer_bytes() / sec / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
+            "us_per_call": sec * 1e6,
+            "sample": (f"one layer of the headline step (B=32, ctx 2048, fp16, block 256) through the "
+                       f"reference's torch decode path (fallback.py:27-64, restated in oracle/paged_oracle.py); "
+                       f"median of {len(samples)} runs after 1 warm-up; torch threads={threads}, "
+                       f"os.cpu_count()={os.cpu_count()}, cpu={cpu_model}")}
+
+
+# ---------------------------------------------------------------------------
+# Other workloads of the path (reported under "extra").
+# ---------------------------------------------------------------------------
+
+def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, oracle):
+    dev = torch.device("cuda:0")
+    extra = {}
+
+    # B=1 / ctx 128, fp16, block 256.
+    c = workloads.decode_b1(dev)
+    out = torch.empty_like(c["query"])
+    fn = lambda: paged_attention(c["query"], c["key_cache"], c["value_cache"], c["block_tables"],  # noqa: E731
+                                 c["context_lens"], 256, backend="hip", validate=False, out=out)
+
+    def many(n=50):
+        def run():
+            for _ in range(n):
+                fn()
+        return run
+    ms, _ = graph_time_ms(many(), torch, calls_per_graph=50, replays=20, warmup=3)
+    ref = oracle.fp32_oracle({k: c[k].cpu() for k in oracle.TENSOR_NAMES}, 256)
+    bytes_b1 = 1 * 128 * 4096 + 2 * 16 * 128 * 2 + 8 + 8
+    extra["decode_b1_ctx128_fp16"] = {"us_per_call": ms / 50 * 1e3, "GBps": bytes_b1 / (ms / 50 * 1e-3) / 1e9,
+                                      "max_abs_error": max_abs(out, ref), "reference_rtx5080_us": 18.945}
+
+    # B=8 / ctx 512, bf16, block 16, + scatter of the new token.
+    c = workloads.decode_b8_with_scatter(dev)
+    out = torch.empty_like(c["query"])
+
+    def scatter_decode():
+        write_kv_cache_slots(c["key_cache"], c["value_cache"], c["slot_mapping"], c["new_key"], c["new_value"],
+                             backend="hip", validate=False)
+        paged_attention(c["query"], c["key_cache"], c["value_cache"], c["block_tables"], c["context_lens"], 16,
+                        backend="hip", validate=False, out=out)
+
+    def many2(n=50):
+        def run():
+            for _ in range(n):
+                scatter_decode()
+        return run
+    ms, _ = graph_time_ms(many2(), torch, calls_per_graph=50, replays=20, warmup=3)
+    kc, vc = c["key_cache"].cpu(), c["value_cache"].cpu()
+    slots_ok = torch.equal(kc.view(-1, 8, 128)[c["slot_mapping"].cpu()], c["new_key"].cpu())
+    ref = oracle.fp32_oracle({"query": c["query"].cpu(), "key_cache": kc, "value_cache": vc,
+                              "block_tables": c["block_tables"].cpu(), "context_lens": c["context_lens"].cpu()}, 16)
+    bytes_b8 = 8 * 512 * 4096 + 2 * 8 * 16 * 128 * 2 + 8 * 32 * 8 + 8 * 8
+    extra["decode_b8_ctx512_bf16_with_scatter"] = {
+        "us_per_call": ms / 50 * 1e3, "GBps_decode_bytes": bytes_b8 / (ms / 50 * 1e-3) / 1e9,
+        "scatter_bit_exact": bool(slots_ok), "max_abs_error": max_abs(out, ref), "reference_rtx5080_us": 40.340}
+
+    # Ragged B=64, ctx U[1,4096], bf16, block 16, shared 1024-token prefix.
+    c = workloads.ragged_shared_prefix_case(device=dev)
+    out = torch.empty_like(c["query"])
+    fn4 = lambda: paged_attention(c["query"], c["key_cache"], c["value_cache"], c["block_tables"],  # noqa: E731
+                                  c["context_lens"], 16, backend="hip", validate=False, out=out)
+
+    def many4(n=10):
+        def run():
+            for _ in range(n):
+                fn4()
+        return run
+    ms, _ = graph_time_ms(many4(), torch, calls_per_graph=10, replays=10, warmup=2)
+    per_call = ms / 10 * 1e-3
+    unique = c["unique_rows"] * 4096 + 2 * 64 * 16 * 128 * 2 + 64 * 256 * 8 + 64 * 8
+    logical = c["logical_rows"] * 4096 + 2 * 64 * 16 * 128 * 2 + 64 * 256 * 8 + 64 * 8
+    ref = oracle.fp32_oracle({k: c[k].cpu() for k in oracle.TENSOR_NAMES}, 16)
+    extra["ragged_b64_shared_prefix_bf16"] = {
+        "us_per_call": per_call * 1e6, "GBps_unique": unique / per_call / 1e9,
+        "frac_of_hbm_peak_unique": unique / per_call / 1e9 / HBM_PEAK_GBS,
+        "GBps_logical": logical / per_call / 1e9, "unique_rows": c["unique_rows"], "logical_rows": c["logical_rows"],
+        "max_abs_error": max_abs(out, ref)}
+
+    # Chunked prefill: 8 x 128 new tokens after U[0,3968] prior, bf16, block 256.
+    c = workloads.chunked_prefill_case(device=dev)
+    names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+    write_kv_cache_slots(c["key_cache"], c["value_cache"], c["slot_mapping"], c["new_key"], c["new_value"],
+                         backend="hip", validate=False)
+    pargs = [c[n] for n in names]
+    holder = {}
+
+    def pf():
+        holder["out"] = paged_prefill_attention(*pargs, 256, backend="hip", validate=False)
+
+    def many5(n=10):
+        def run():
+            for _ in range(n):
+                pf()
+        return run
+    ms, _ = graph_time_ms(many5(), torch, calls_per_graph=10, replays=10, warmup=2)
+    per_call = ms / 10 * 1e-3
+    flops = workloads.prefill_flops(c["priors"])
+    kv_bytes = sum(p + 128 for p in c["priors"]) * 4096 + 2 * 1024 * 16 * 128 * 2
+    ref = oracle.paged_prefill_attention(*[a.cpu() for a in pargs], 256, cast=False)
+    extra["chunked_prefill_8x128_bf16"] = {
+        "us_per_call": per_call * 1e6, "TFLOPs": flops / per_call / 1e12,
+        "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "GBps": kv_bytes / per_call / 1e9, "flops": flops, "priors": c["priors"],
+        "max_abs_error": max_abs(holder["out"], ref)}
+    return extra
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = library default)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's paged-attention path runs on a single MI355X "
+              f"(--gpus {args.gpus} is not supported; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from mini_engine_hip.kernels import hip_extension
+    from mini_engine_hip.kernels.data import write_kv_cache_slots
+    from mini_engine_hip.kernels.paged import paged_attention
+    from mini_engine_hip.kernels.prefill import paged_prefill_attention
+    from mini_engine_hip import workloads
+    from oracle import paged_oracle
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    lib = hip_extension.load_hip_extension()
+    log(f"library {lib.path}")
+
+    layers, step_ms, eager_ms = headline(args, torch, paged_attention, workloads)
+    per_call_ms = step_ms / LAYERS
+    step_bytes = LAYERS * layer_bytes()
+    achieved_gbs = layer_bytes() / (per_call_ms * 1e-3) / 1e9
+    log(f"headline: {step_ms:.3f} ms/step, {per_call_ms * 1e3:.2f} us/call, {achieved_gbs:.0f} GB/s")
+    parity = headline_parity(layers, paged_oracle)
+    log(f"parity: {parity}")
+
+    traffic = None
+    traffic_file = ROOT / "profiles" / "paged_decode_b32_ctx2048_traffic.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+
+    result = {
+        "metric": METRIC,
+        "value": step_bytes / (step_ms * 1e-3) / 1e12,
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "us_per_call": per_call_ms * 1e3,
+        "eager_wall_us_per_call": eager_ms / LAYERS * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic N(0,1) q/K/V, seeded random non-contiguous pages; inputs resident in HBM",
+        "config": {"workload": "paged_decode_b32_ctx2048_fp16_block256_28layers", "batch": BATCH,
+                   "context": CONTEXT, "q_heads": HQ, "kv_heads": HKV, "head_dim": D, "block_size": BLOCK,
+                   "layers": LAYERS, "kv_pool_per_layer": "263 pages, separate per layer",
+                   "algorithmic_bytes_per_call": layer_bytes(), "timing": "hipGraph of 28 calls per step"},
+        "roofline": {"bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel": "paged_decode_kernel (fp16, D=128, G=2, 16 waves)"},
+        "parity": parity,
+        "reference_published": {"us_per_call_rtx5080": REFERENCE_US_PER_CALL,
+                                "speedup_vs_rtx5080": REFERENCE_US_PER_CALL / (per_call_ms * 1e3)},
+    }
+    del layers
+    torch.cuda.empty_cache()
+    if not args.no_extra:
+        result["extra"] = extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention,
+                                          workloads, paged_oracle)
+        log(f"extra: {json.dumps(result['extra'])}")
+    if not args.no_cpu_baseline:
+        gen_layers = [workloads.decode_b32_layer(torch.device("cuda:0"), seed=BASE_SEED + 2)]
+        result["cpu_baseline"] = cpu_baseline(gen_layers, paged_oracle, torch, args.cpu_budget)
+        log(f"cpu baseline: {result['cpu_baseline']}")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,9 +1,13 @@
 // GQA paged decode attention for gfx950.
 //
-// Work decomposition: one work-group (4 waves, 256 lanes) per
+// Work decomposition: one work-group of NW waves per
 // (sequence, kv head, G-query-head tile, partition of `partition` tokens).
 // All G query heads that share a kv head are served by the same loads, so
-// every K/V byte of a partition is fetched from HBM exactly once.
+// every K/V byte of a partition is fetched from HBM exactly once.  When the
+// (sequence, kv head) units alone fill the GPU, a 16-wave work-group covers a
+// whole sequence and merges its waves in LDS: one kernel, no workspace.
+// Otherwise the context is split into partitions of 4-wave work-groups
+// (split-K) whose fp32 partials a second, small kernel merges.
 //
 // Lane layout inside a wave: a token row of one kv head is head_dim*2 bytes
 // = D/8 16-byte chunks; LPT (next power of two >= D/8) consecutive lanes
@@ -15,17 +19,15 @@
 // 8 elements, then a DPP reduction across the LPT lanes of the token.
 // Softmax: online, fp32, base-2 exponent with log2(e)/sqrt(D) folded into
 // the scale.  Each token group of lanes keeps its own running max/sum/acc;
-// groups, then waves (through LDS), are merged at the end.
-// Split-K: partitions > 1 write fp32 (acc, max, sum) partials and a merge
-// kernel combines them; sequences that fit one partition write the output
-// directly from the attention kernel.
+// groups, then waves (through LDS), are merged at the end.  Sequences that
+// fit one partition write the output directly from the attention kernel.
 #include "mvme_common.h"
 
 namespace mvme {
 namespace {
 
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeThreads = kDecodeWaves * kWave;
+constexpr int kSplitWaves = 4;   // waves per work-group in split-K mode
+constexpr int kWholeWaves = 16;  // waves per work-group covering a whole sequence
 constexpr int kDecodeLoads = 4;  // K (and V) loads per lane per iteration
 
 template <int D>
@@ -35,7 +37,6 @@ struct DecodeShape {
                               : kChunks <= 8 ? 8 : kChunks <= 16 ? 16 : kChunks <= 32 ? 32 : 64;
     static constexpr int kTpl = kWave / kLpt;          // tokens per load
     static constexpr int kTpi = kTpl * kDecodeLoads;   // tokens per wave iteration
-    static constexpr int kStep = kTpi * kDecodeWaves;  // tokens per work-group iteration
 };
 
 struct DecodeArgs {
@@ -55,7 +56,7 @@ struct DecodeArgs {
     int block_size;
     int table_width;
     int capacity;   // table_width * block_size
-    int partition;  // tokens per partition (multiple of DecodeShape::kStep)
+    int partition;  // tokens per partition (multiple of the wave tile)
     int max_parts;
     float scale_log2;
 };
@@ -66,10 +67,11 @@ __device__ inline int seq_tokens(int64_t len64, int capacity) {
     return (len64 > 0 && len64 <= capacity) ? (int)len64 : 0;
 }
 
-template <typename T, int D, int G, bool PAGE_UNIFORM>
-__global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs a) {
+template <typename T, int D, int G, bool PAGE_UNIFORM, int NW>
+__global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) {
     using S = DecodeShape<D>;
     constexpr int L = kDecodeLoads;
+    constexpr int kStep = S::kTpi * NW;  // tokens per work-group iteration
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = threadIdx.x / kWave;
     const int tl = lane / S::kLpt;  // token slot inside one load
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
     const uint16_t* vbase = static_cast<const uint16_t*>(a.value_cache) + kvh * D + 8 * c;
     const int64_t* table = a.tables + (int64_t)b * a.table_width;
 
-    for (int it = start + wave * S::kTpi; it < end; it += S::kStep) {
+    for (int it = start + wave * S::kTpi; it < end; it += kStep) {
         u32x4 kk[L], vv[L];
         bool ok[L];
         if constexpr (PAGE_UNIFORM) {
@@ -213,8 +215,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
     }
 
     // Merge the waves through LDS.
-    __shared__ float sm_acc[kDecodeWaves][G][D];
-    __shared__ float sm_ml[kDecodeWaves][G][2];
+    __shared__ float sm_acc[NW][G][D];
+    __shared__ float sm_ml[NW][G][2];
     if (tl == 0 && chunk_ok) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -228,16 +230,16 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
     }
     __syncthreads();
 
-    for (int idx = threadIdx.x; idx < G * D; idx += kDecodeThreads) {
+    for (int idx = threadIdx.x; idx < G * D; idx += NW * kWave) {
         const int g = idx / D;
         const int d = idx - g * D;
         float mx = sm_ml[0][g][0];
 #pragma unroll
-        for (int w = 1; w < kDecodeWaves; ++w) mx = fmaxf(mx, sm_ml[w][g][0]);
+        for (int w = 1; w < NW; ++w) mx = fmaxf(mx, sm_ml[w][g][0]);
         const float ref = mx == kNegInf ? 0.f : mx;
         float sum = 0.f, o = 0.f;
 #pragma unroll
-        for (int w = 0; w < kDecodeWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             const float f = fast_exp2(sm_ml[w][g][0] - ref);
             sum += sm_ml[w][g][1] * f;
             o += sm_acc[w][g][d] * f;
@@ -284,85 +286,101 @@ struct DecodePlan {
     int partition;
     int max_parts;
     int gtile;  // G of the kernel instance
-    int step;
+    int waves;  // waves per work-group (kSplitWaves or kWholeWaves)
 };
 
-int decode_step_tokens(int64_t head_dim) {
+int decode_tile_tokens(int64_t head_dim) {
     switch (head_dim) {
-        case 16: return DecodeShape<16>::kStep;
-        case 32: return DecodeShape<32>::kStep;
-        case 64: return DecodeShape<64>::kStep;
-        case 80: return DecodeShape<80>::kStep;
-        case 96: return DecodeShape<96>::kStep;
-        case 128: return DecodeShape<128>::kStep;
-        case 192: return DecodeShape<192>::kStep;
-        case 256: return DecodeShape<256>::kStep;
+        case 16: return DecodeShape<16>::kTpi;
+        case 32: return DecodeShape<32>::kTpi;
+        case 64: return DecodeShape<64>::kTpi;
+        case 80: return DecodeShape<80>::kTpi;
+        case 96: return DecodeShape<96>::kTpi;
+        case 128: return DecodeShape<128>::kTpi;
+        case 192: return DecodeShape<192>::kTpi;
+        case 256: return DecodeShape<256>::kTpi;
         default: return 0;
     }
 }
 
-int decode_tile_tokens(int64_t head_dim) { return decode_step_tokens(head_dim) / kDecodeWaves; }
+constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 
-// Host-side partition choice: enough work-groups to give every CU several
-// waves (the whole table capacity counted, since lengths stay on the device)
-// while keeping partitions long enough to amortise the merge.
+// Host-side plan (lengths stay on the device, so it depends on the table
+// capacity only).  Enough (sequence, kv head) units to occupy every CU: one
+// 16-wave work-group per unit over the whole context, merged in LDS.
+// Fewer units: split-K into partitions of 4-wave work-groups, sized to give
+// every CU about four work-groups, plus a merge kernel.  `requested` > 0
+// forces split-K with that partition length (rounded to the wave tiling).
 DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                             int64_t block_size, int64_t table_width, int64_t requested) {
     DecodePlan p{};
     const int64_t group = q_heads / kv_heads;
     p.gtile = group % 4 == 0 ? 4 : group % 2 == 0 ? 2 : 1;
-    p.step = decode_step_tokens(head_dim);
+    const int64_t tile = decode_tile_tokens(head_dim);
     const int64_t cap = table_width * block_size;
-    const int64_t cap_steps = (cap + p.step - 1) / p.step * p.step;
+    const int64_t units = batch * kv_heads * (group / p.gtile);
+    const int64_t split_step = tile * kSplitWaves;
+    const int64_t whole_step = tile * kWholeWaves;
     int64_t part;
-    if (requested > 0) {
-        part = (requested + p.step - 1) / p.step * p.step;
+    if (requested <= 0 && (units >= kDeviceCUs - kDeviceCUs / 16 || cap * units <= 64 * 1024)) {
+        // Whole-sequence work-groups (also the launch-bound tiny case).
+        p.waves = cap >= 4 * whole_step ? kWholeWaves : kSplitWaves;
+        part = (cap + tile - 1) / tile * tile;
     } else {
-        const int64_t units = batch * kv_heads * (group / p.gtile);
-        constexpr int64_t kTargetGroups = 1024;  // 256 CUs x 4 work-groups
-        part = (cap * units + kTargetGroups - 1) / kTargetGroups;
-        part = (part + p.step - 1) / p.step * p.step;
-        if (part < 256) part = 256;  // short partitions only add merge traffic
-        // Small problems are launch-bound: one partition avoids the merge launch.
-        if (cap * units <= 64 * 1024) part = cap_steps;
+        p.waves = kSplitWaves;
+        if (requested > 0) {
+            part = requested;
+        } else {
+            constexpr int64_t kTargetGroups = 4 * kDeviceCUs;
+            part = (cap * units + kTargetGroups - 1) / kTargetGroups;
+            if (part < 256) part = 256;  // short partitions only add merge traffic
+        }
+        part = (part + split_step - 1) / split_step * split_step;
+        const int64_t cap_steps = (cap + split_step - 1) / split_step * split_step;
+        if (part > cap_steps) part = cap_steps;
     }
-    if (part < p.step) part = p.step;
-    if (part > cap_steps) part = cap_steps;
     p.partition = (int)part;
     p.max_parts = (int)((cap + part - 1) / part);
     return p;
 }
 
-template <typename T, int D, int G>
-void launch_decode(const DecodeArgs& a, int units, bool page_uniform, hipStream_t s) {
+template <typename T, int D, int G, int NW>
+void launch_decode_nw(const DecodeArgs& a, int units, bool page_uniform, hipStream_t s) {
     const dim3 grid(units, a.max_parts);
     if (page_uniform)
-        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, true>), grid, dim3(kDecodeThreads), 0, s, a);
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, true, NW>), grid, dim3(NW * kWave), 0, s, a);
     else
-        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, false>), grid, dim3(kDecodeThreads), 0, s, a);
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, false, NW>), grid, dim3(NW * kWave), 0, s, a);
+}
+
+template <typename T, int D, int G>
+void launch_decode(const DecodeArgs& a, int waves, int units, bool page_uniform, hipStream_t s) {
+    if (waves == kWholeWaves) launch_decode_nw<T, D, G, kWholeWaves>(a, units, page_uniform, s);
+    else launch_decode_nw<T, D, G, kSplitWaves>(a, units, page_uniform, s);
     if (a.max_parts > 1)
         hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(units / a.kv_heads / a.gtiles * a.q_heads),
                            dim3(D < 256 ? D : 256), 0, s, a);
 }
 
 template <typename T, int D>
-void launch_decode_g(const DecodeArgs& a, int gtile, int units, bool page_uniform, hipStream_t s) {
-    if (gtile == 4) launch_decode<T, D, 4>(a, units, page_uniform, s);
-    else if (gtile == 2) launch_decode<T, D, 2>(a, units, page_uniform, s);
-    else launch_decode<T, D, 1>(a, units, page_uniform, s);
+void launch_decode_g(const DecodeArgs& a, const DecodePlan& p, int units, bool page_uniform, hipStream_t s) {
+    if (p.gtile == 4) launch_decode<T, D, 4>(a, p.waves, units, page_uniform, s);
+    else if (p.gtile == 2) launch_decode<T, D, 2>(a, p.waves, units, page_uniform, s);
+    else launch_decode<T, D, 1>(a, p.waves, units, page_uniform, s);
 }
 
 template <typename T>
-void launch_decode_d(const DecodeArgs& a, int64_t head_dim, int gtile, int units, bool pu, hipStream_t s) {
+void launch_decode_d(const DecodeArgs& a, int64_t head_dim, const DecodePlan& p, int units, bool pu,
+                     hipStream_t s) {
     switch (head_dim) {
-        case 16: launch_decode_g<T, 16>(a, gtile, units, pu, s); break;
-        case 32: launch_decode_g<T, 32>(a, gtile, units, pu, s); break;
-        case 64: launch_decode_g<T, 64>(a, gtile, units, pu, s); break;
-        case 80: launch_decode_g<T, 80>(a, gtile, units, pu, s); break;
-        case 96: launch_decode_g<T, 96>(a, gtile, units, pu, s); break;
-        case 128: launch_decode_g<T, 128>(a, gtile, units, pu, s); break;
-        case 192: launch_decode_g<T, 192>(a, gtile, units, pu, s); break;
-        case 256: launch_decode_g<T, 256>(a, gtile, units, pu, s); break;
+        case 16: launch_decode_g<T, 16>(a, p, units, pu, s); break;
+        case 32: launch_decode_g<T, 32>(a, p, units, pu, s); break;
+        case 64: launch_decode_g<T, 64>(a, p, units, pu, s); break;
+        case 80: launch_decode_g<T, 80>(a, p, units, pu, s); break;
+        case 96: launch_decode_g<T, 96>(a, p, units, pu, s); break;
+        case 128: launch_decode_g<T, 128>(a, p, units, pu, s); break;
+        case 192: launch_decode_g<T, 192>(a, p, units, pu, s); break;
+        case 256: launch_decode_g<T, 256>(a, p, units, pu, s); break;
     }
 }
 
@@ -373,7 +391,7 @@ int check_decode_shapes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_
         return fail(MVME_EINVAL, "empty batch/heads/cache");
     if (block_size <= 0) return fail(MVME_EINVAL, "block size mismatch");
     if (q_heads % kv_heads != 0) return fail(MVME_EINVAL, "head dimension or GQA mismatch");
-    if (decode_step_tokens(head_dim) == 0)
+    if (decode_tile_tokens(head_dim) == 0)
         return fail(MVME_EINVAL, "supported head_dim: 16,32,64,80,96,128,192,256");
     if (table_width <= 0) return fail(MVME_EINVAL, "invalid block table");
     if (table_width * block_size > 1048576) return fail(MVME_EINVAL, "maximum table capacity is 1M tokens");
@@ -390,7 +408,7 @@ extern "C" size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_h
                                                       int64_t head_dim, int64_t block_size,
                                                       int64_t table_width, int64_t partition_tokens) {
     if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || block_size <= 0 ||
-        table_width <= 0 || decode_step_tokens(head_dim) == 0)
+        table_width <= 0 || decode_tile_tokens(head_dim) == 0)
         return 0;
     const DecodePlan p = make_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, table_width,
                                           partition_tokens);
@@ -443,7 +461,7 @@ extern "C" int mvme_paged_attention(void* out, const void* query, const void* ke
     a.scale_log2 = kLog2e / sqrtf((float)head_dim);
     const bool page_uniform = block_size % decode_tile_tokens(head_dim) == 0;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (dtype == MVME_FP16) launch_decode_d<Half>(a, head_dim, p.gtile, (int)units, page_uniform, s);
-    else launch_decode_d<BFloat16>(a, head_dim, p.gtile, (int)units, page_uniform, s);
+    if (dtype == MVME_FP16) launch_decode_d<Half>(a, head_dim, p, (int)units, page_uniform, s);
+    else launch_decode_d<BFloat16>(a, head_dim, p, (int)units, page_uniform, s);
     return check_launch("paged attention");
 }
