@@ -269,6 +269,8 @@ def main(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 10 plain 1 GiB device copies (scale reference for HBM byte counters)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's paged-attention path runs on a single MI355X "
@@ -286,6 +288,15 @@ def main(argv=None):
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
+    if args.copy_calibration:
+        src = torch.ones(1 << 29, dtype=torch.float16, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": src.numel() * 2, "copy_calibration_bytes_written":
+                          dst.numel() * 2, "copies": 10}))
+        return 0
     lib = hip_extension.load_hip_extension()
     log(f"library {lib.path}")
 
@@ -298,9 +309,11 @@ def main(argv=None):
     log(f"parity: {parity}")
 
     traffic = None
-    traffic_file = ROOT / "profiles" / "paged_decode_b32_ctx2048_traffic.json"
+    traffic_file = ROOT / "profiles" / "paged_decode_b32_ctx2048_traffic.txt"
     if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get("hbm_bytes_per_launch")
+        for line in traffic_file.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_launch:"):
+                traffic = int(line.split(":", 1)[1])
 
     result = {
         "metric": METRIC,

@@ -1,0 +1,108 @@
+"""C-ABI library checks that need no GPU.
+
+The library must load, export every entry point that include/mvme_paged.h
+declares, report its ABI version, and reject bad arguments with a status
+code and a message *before* launching anything (these calls never reach a
+kernel).  The Python layer must fail loudly when the library is missing.
+"""
+
+import ctypes
+from pathlib import Path
+import re
+
+import pytest
+
+from mini_engine_hip import build as hip_build
+from mini_engine_hip.kernels import hip_extension as ext
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "mvme_paged.h"
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mvme_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return ext.load_hip_extension()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    symbols = declared_symbols()
+    assert len(symbols) == 9
+    raw = ctypes.CDLL(str(hip_build.library_path()))
+    for name in symbols:
+        assert hasattr(raw, name), name
+    assert set(ext.SIGNATURES) == set(symbols)
+
+
+def test_abi_version(lib):
+    assert lib._lib.mvme_abi_version() == ext.ABI_VERSION == 1
+
+
+def test_workspace_size_is_a_host_function(lib):
+    # Headline decode (B=32, ctx 2048, block 256): one work-group per unit, no split.
+    assert lib.workspace_size(32, 16, 8, 128, 256, 8, 0) == 0
+    # Few units: split-K partials of fp32 (acc[D] + max + sum) per partition.
+    size = lib.workspace_size(1, 16, 8, 128, 16, 256, 512)
+    assert size == 1 * 16 * 8 * (128 + 2) * 4
+    assert lib.workspace_size(1, 16, 8, 100, 16, 256, 0) == 0  # unsupported head dim
+
+
+def _status(lib, name, *args):
+    return getattr(lib._lib, name)(*args)
+
+
+def test_decode_rejects_bad_arguments_before_launch(lib):
+    base = dict(batch=2, q_heads=16, kv_heads=8, head_dim=128, num_blocks=4, block_size=16, table_width=2)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return _status(lib, "mvme_paged_attention", 1, 1, 1, 1, 1, 1, a["batch"], a["q_heads"], a["kv_heads"],
+                       a["head_dim"], a["num_blocks"], a["block_size"], a["table_width"], 0, kw.get("dtype", 0),
+                       None, 0, None)
+
+    assert call(dtype=7) == ext.EINVAL and "FP16/BF16" in lib.last_error()
+    assert call(head_dim=100) == ext.EINVAL and "head_dim" in lib.last_error()
+    assert call(q_heads=12, kv_heads=8) == ext.EINVAL and "GQA" in lib.last_error()
+    assert call(table_width=70000, block_size=16) == ext.EINVAL and "1M" in lib.last_error()
+    assert call(batch=0) == ext.EINVAL and "empty" in lib.last_error()
+    # Split-K shape without workspace.
+    status = _status(lib, "mvme_paged_attention", 1, 1, 1, 1, 1, 1, 1, 16, 8, 128, 64, 16, 256, 512, 0, None, 0,
+                     None)
+    assert status == ext.EWORKSPACE and "workspace" in lib.last_error()
+    assert _status(lib, "mvme_paged_attention", None, 1, 1, 1, 1, 1, 2, 16, 8, 128, 4, 16, 2, 0, 0, None, 0,
+                   None) == ext.EINVAL
+
+
+def test_scatter_and_prefill_reject_bad_arguments(lib):
+    assert _status(lib, "mvme_write_kv_cache_slots", 1, 1, 0, 16, 8, 128, 1, 1, 1, 4, 1024, 1024, 0, None) == ext.EINVAL
+    assert _status(lib, "mvme_write_kv_cache_slots", 1, 1, 4, 16, 8, 128, 1, 1, 1, 4, 100, 1024, 0, None) == ext.EINVAL
+    assert "stride" in lib.last_error()
+    assert _status(lib, "mvme_write_kv_cache", 1, 1, 4, 16, 8, 128, 1, 2, 30, 1, 1, 5, 1, None) == ext.EINVAL
+    assert "exceeds" in lib.last_error()
+    assert _status(lib, "mvme_paged_prefill_attention", 1, 1, 1, 1, 1, 1, 1, 1, 1, 4, 16, 8, 2048, 4, 16, 1, 0,
+                   None) == ext.EINVAL
+    assert "1024" in lib.last_error()
+    # Empty inputs are legal no-ops.
+    assert _status(lib, "mvme_write_kv_cache_slots", 1, 1, 4, 16, 8, 128, None, None, None, 0, 1024, 1024, 1,
+                   None) == ext.OK
+    assert _status(lib, "mvme_paged_prefill_attention", None, None, None, None, None, None, None, None, 0, 0, 16, 8,
+                   128, 4, 16, 0, 1, None) == ext.OK
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """No silent fallback: without a buildable library every call raises."""
+    ext.load_hip_extension.cache_clear()
+    monkeypatch.setattr(hip_build, "library_path", lambda: tmp_path / "libmissing.so")
+
+    def refuse(**_):
+        raise RuntimeError("hipcc not found: the HIP library cannot be built")
+
+    monkeypatch.setattr(hip_build, "build_library", refuse)
+    try:
+        with pytest.raises(RuntimeError, match="cannot be built"):
+            ext.load_hip_extension()
+    finally:
+        ext.load_hip_extension.cache_clear()

@@ -1,0 +1,161 @@
+"""Host-side contract checks of the hip backend entry points (CPU only).
+
+These mirror the reference's pre-dispatch validation tests
+(tests/test_ragged_kernels.py:48-99, tests/test_ragged_model.py:42-73): the
+same ValueError messages fire before any kernel could run, and CPU tensors
+are refused by the hip backend instead of being computed on the CPU.
+"""
+
+import pytest
+import torch
+
+from mini_engine_hip.cache.page_pool import PagePool
+from mini_engine_hip.engine.batch import PrefillBatch
+from mini_engine_hip.kernels.data import write_kv_cache, write_kv_cache_batch, write_kv_cache_slots
+from mini_engine_hip.kernels.paged import paged_attention
+from mini_engine_hip.kernels.prefill import paged_prefill_attention
+from oracle import paged_oracle
+
+
+def inputs(dtype=torch.float16, dim=16):
+    gen = torch.Generator().manual_seed(631)
+    key = torch.randn(8, 4, 2, dim, generator=gen).to(dtype)
+    value = torch.randn(8, 4, 2, dim, generator=gen).to(dtype)
+    q = torch.randn(8, 4, dim, generator=gen).to(dtype)
+    meta = [torch.tensor(x, dtype=torch.int64) for x in ([0, 3, 8], [5, 1], [[5, 1, -1], [2, 7, -1]], [8, 6])]
+    return [q, key, value, *meta]
+
+
+def test_only_the_hip_backend_is_served():
+    q, key, value, *_ = inputs()
+    with pytest.raises(ValueError, match="hip"):
+        paged_attention(q[:2], key, value, torch.zeros(2, 1, dtype=torch.long), torch.ones(2, dtype=torch.long), 4,
+                        backend="torch")
+    with pytest.raises(ValueError, match="hip"):
+        write_kv_cache_slots(key, value, torch.tensor([0]), key[0, :1], value[0, :1], backend="cuda")
+    with pytest.raises(ValueError, match="hip"):
+        paged_prefill_attention(*inputs(), 4, backend="torch")
+
+
+def test_cpu_tensors_are_refused_not_computed():
+    q, key, value, *_ = inputs()
+    with pytest.raises(ValueError, match="FP16/BF16"):
+        paged_attention(q.float()[:2], key, value, torch.zeros(2, 1, dtype=torch.long),
+                        torch.ones(2, dtype=torch.long), 4)
+    with pytest.raises(RuntimeError, match="query must be CUDA"):
+        paged_attention(q[:2], key, value, torch.zeros(2, 1, dtype=torch.long), torch.ones(2, dtype=torch.long), 4)
+    with pytest.raises(ValueError, match="HIP packed KV"):
+        write_kv_cache_slots(key, value, torch.tensor([3]), torch.ones(1, 2, 16).half(), torch.ones(1, 2, 16).half())
+    with pytest.raises(ValueError, match="HIP paged prefill"):
+        paged_prefill_attention(*inputs(), 4)
+
+
+def test_slot_scatter_rejects_races_before_mutation():
+    """test_ragged_kernels.py:48-65: duplicate slots, overlap, capacity."""
+    _, key, value, *_ = inputs()
+    before = key.clone()
+    source = torch.randn(8, 2, 16).half()
+    with pytest.raises(ValueError, match="duplicate"):
+        write_kv_cache_slots(key, value, torch.zeros(8, dtype=torch.int64), source, source)
+    slots = torch.tensor([5, 6, 7, 9, 10, 11, 28, 29], dtype=torch.int64)
+    with pytest.raises(ValueError, match="overlap"):
+        write_kv_cache_slots(key, value, slots, key.view(-1, 2, 16)[:8], source)
+    with pytest.raises(ValueError, match="overlap"):
+        write_kv_cache_slots(key, key, slots, source, source)
+    for slot in (-1, 32):
+        with pytest.raises(ValueError, match="capacity"):
+            write_kv_cache_slots(key, value, torch.tensor([slot]), torch.ones(1, 2, 16).half(),
+                                 torch.ones(1, 2, 16).half())
+    with pytest.raises(ValueError, match="int64"):
+        write_kv_cache_slots(key, value, slots.int(), source, source)
+    assert torch.equal(key, before)
+
+
+@pytest.mark.parametrize("change,message", [
+    (lambda a: a[3].fill_(0), "offset"),
+    (lambda a: a[4].fill_(-1), "context"),
+    (lambda a: a[6].fill_(99), "capacity"),
+    (lambda a: a[5].fill_(-1), "physical"),
+    (lambda a: a[5].fill_(8), "physical"),
+    (lambda a: a.__setitem__(3, a[3].to(torch.int32)), "int64"),
+])
+def test_invalid_paged_metadata_rejected_before_dispatch(change, message):
+    """test_ragged_kernels.py:68-80 for the hip backend."""
+    args = inputs()
+    change(args)
+    with pytest.raises(ValueError, match=message):
+        paged_prefill_attention(*args, 4, backend="hip")
+
+
+def test_range_and_batch_write_contracts():
+    _, key, value, *_ = inputs()
+    with pytest.raises(ValueError, match="capacity"):
+        write_kv_cache(key, value, torch.tensor([1, 2]), 6, torch.ones(3, 2, 16).half(), torch.ones(3, 2, 16).half(), 4)
+    with pytest.raises(ValueError, match="shape mismatch"):
+        write_kv_cache_batch(key, value, torch.zeros(3, 2, dtype=torch.long), torch.zeros(2, dtype=torch.long),
+                             torch.ones(2, 2, 16).half(), torch.ones(2, 2, 16).half(), 4)
+    with pytest.raises(RuntimeError, match="CUDA"):
+        write_kv_cache(key, value, torch.tensor([1, 2]), 0, torch.ones(3, 2, 16).half(), torch.ones(3, 2, 16).half(), 4)
+
+
+# ---------------------------------------------------------------------------
+# PrefillBatch: the reference's KAT and rejection table (test_ragged_model.py:42-73)
+# ---------------------------------------------------------------------------
+
+def metadata(sequences, tables, starts, num_blocks=16):
+    return PrefillBatch.from_sequences(sequences, tables, starts, block_size=4, num_blocks=num_blocks, device="cpu")
+
+
+def test_prefill_metadata_positions_slots_and_readonly_prefix_sharing():
+    batch = metadata([[5, 6, 7], [8, 9]], [[3, 1, -1], [3, 2]], [4, 4])
+    assert batch.query_lengths == (3, 2) and batch.query_offsets == (0, 3, 5)
+    assert batch.starts == (4, 4) and batch.block_ids == ((3, 1), (3, 2))
+    assert batch.block_size == 4 and batch.batch_size == 2 and batch.num_tokens == 5
+    assert batch.input_ids.tolist() == [5, 6, 7, 8, 9]
+    assert batch.positions.tolist() == [4, 5, 6, 4, 5]
+    assert batch.slot_mapping.tolist() == [4, 5, 6, 8, 9]
+    assert batch.cu_seqlens_q.tolist() == [0, 3, 5]
+    assert batch.context_lens.tolist() == [7, 6]
+    assert batch.block_tables.tolist() == [[3, 1], [3, 2]]
+    # Agrees with the oracle's restatement of the same rules.
+    ref = paged_oracle.prefill_metadata([[5, 6, 7], [8, 9]], [[3, 1, -1], [3, 2]], [4, 4], 4)
+    assert batch.slot_mapping.tolist() == ref["slot_mapping"] and batch.positions.tolist() == ref["positions"]
+
+
+@pytest.mark.parametrize("sequences,tables,starts,error", [
+    ([[]], [[0]], [0], "nonempty"),
+    ([[1]], [[0]], [-1], "nonnegative"),
+    ([[1]], [[0]], [True], "integers"),
+    ([[1]], [[0]], [], "equal batch"),
+    ([[-1]], [[0]], [0], "nonnegative"),
+    ([[1]], [[16]], [0], "out of range"),
+    ([[1]], [[0, 0]], [0], "duplicate physical"),
+    ([[1]], [[0, -1, 2]], [0], "trailing"),
+    ([[1, 2]], [[0]], [3], "capacity"),
+    ([[1], [2]], [[0], [0]], [0, 0], "duplicate writable"),
+    ([[1], [2]], [[0], [0]], [0, 1], "shared by requests"),
+    ([torch.tensor([1.0])], [[0]], [0], "int64"),
+    ([[1 << 64]], [[0]], [0], "int64"),
+])
+def test_prefill_metadata_rejects_invalid_layout(sequences, tables, starts, error):
+    with pytest.raises(ValueError, match=error):
+        metadata(sequences, tables, starts)
+
+
+def test_page_pool_shared_prefix_refcounts():
+    """block_manager.py:55-105 semantics: a cached prefix attached to several requests."""
+    pool = PagePool(12, 4, order=[5, 3, 11, 0, 1, 2, 4, 6, 7, 8, 9, 10])
+    prefix = pool.allocate("prefix", 8)
+    assert prefix == [5, 3] and pool.refcount(5) == 1
+    a = pool.allocate_with_prefix("a", 10, prefix)
+    b = pool.allocate_with_prefix("b", 9, prefix)
+    assert a[:2] == prefix == b[:2] and len(a) == 3 and len(b) == 3 and a[2] != b[2]
+    assert pool.refcount(5) == 3 and pool.refcount(a[2]) == 1
+    pool.free("a")
+    assert pool.refcount(5) == 2
+    with pytest.raises(ValueError, match="more blocks"):
+        pool.allocate_with_prefix("c", 4, prefix)
+    with pytest.raises(MemoryError):
+        pool.allocate("d", 4 * 20)
+    with pytest.raises(ValueError, match="unallocated"):
+        pool.allocate_with_prefix("e", 12, [a[2]])
