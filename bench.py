@@ -273,8 +273,9 @@ def main(argv=None):
                     help="only run 10 plain 1 GiB device copies (scale reference for HBM byte counters)")
     args = ap.parse_args(argv)
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: this build's paged-attention path runs on a single MI355X "
-              f"(--gpus {args.gpus} is not supported; see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU: the paged-attention path runs on a single MI355X and "
+              f"--gpus {args.gpus} is not supported (decode would shard by sequence or kv head with no "
+              f"exchange; this benchmark does not launch ranks)", file=sys.stderr)
         return 2
 
     import torch
