@@ -163,10 +163,25 @@ def cpu_baseline(layers, oracle, torch, budget_s):
 # Other workloads of the path (reported under "extra").
 # ---------------------------------------------------------------------------
 
-def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, oracle):
+EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill")
+
+
+def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, oracle,
+                    names=EXTRA_NAMES):
     dev = torch.device("cuda:0")
     extra = {}
+    if "decode_b1" in names:
+        _extra_b1(torch, paged_attention, workloads, oracle, dev, extra)
+    if "decode_b8" in names:
+        _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, oracle, dev, extra)
+    if "ragged_b64" in names:
+        _extra_ragged(torch, paged_attention, workloads, oracle, dev, extra)
+    if "prefill" in names:
+        _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, oracle, dev, extra)
+    return extra
 
+
+def _extra_b1(torch, paged_attention, workloads, oracle, dev, extra):
     # B=1 / ctx 128, fp16, block 256.
     c = workloads.decode_b1(dev)
     out = torch.empty_like(c["query"])
@@ -184,6 +199,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
     extra["decode_b1_ctx128_fp16"] = {"us_per_call": ms / 50 * 1e3, "GBps": bytes_b1 / (ms / 50 * 1e-3) / 1e9,
                                       "max_abs_error": max_abs(out, ref), "reference_rtx5080_us": 18.945}
 
+
+def _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, oracle, dev, extra):
     # B=8 / ctx 512, bf16, block 16, + scatter of the new token.
     c = workloads.decode_b8_with_scatter(dev)
     out = torch.empty_like(c["query"])
@@ -209,6 +226,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         "us_per_call": ms / 50 * 1e3, "GBps_decode_bytes": bytes_b8 / (ms / 50 * 1e-3) / 1e9,
         "scatter_bit_exact": bool(slots_ok), "max_abs_error": max_abs(out, ref), "reference_rtx5080_us": 40.340}
 
+
+def _extra_ragged(torch, paged_attention, workloads, oracle, dev, extra):
     # Ragged B=64, ctx U[1,4096], bf16, block 16, shared 1024-token prefix.
     c = workloads.ragged_shared_prefix_case(device=dev)
     out = torch.empty_like(c["query"])
@@ -231,6 +250,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         "GBps_logical": logical / per_call / 1e9, "unique_rows": c["unique_rows"], "logical_rows": c["logical_rows"],
         "max_abs_error": max_abs(out, ref)}
 
+
+def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, oracle, dev, extra):
     # Chunked prefill: 8 x 128 new tokens after U[0,3968] prior, bf16, block 256.
     c = workloads.chunked_prefill_case(device=dev)
     names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
@@ -257,7 +278,6 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "GBps": kv_bytes / per_call / 1e9, "flops": flops, "priors": c["priors"],
         "max_abs_error": max_abs(holder["out"], ref)}
-    return extra
 
 
 def main(argv=None):
@@ -268,6 +288,9 @@ def main(argv=None):
     ap.add_argument("--partition", type=int, default=0, help="split-K partition tokens (0 = library default)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--extra", default=",".join(EXTRA_NAMES),
+                    help="comma-separated subset of the other workloads: " + ",".join(EXTRA_NAMES))
+    ap.add_argument("--no-headline", action="store_true", help="skip the headline decode (profiling runs)")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 1 GiB device copies (scale reference for HBM byte counters)")
@@ -300,6 +323,11 @@ def main(argv=None):
         return 0
     lib = hip_extension.load_hip_extension()
     log(f"library {lib.path}")
+    if args.no_headline:
+        extra = extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads,
+                                paged_oracle, names=tuple(args.extra.split(",")))
+        print(json.dumps({"profiling_run": True, "extra": extra}), flush=True)
+        return 0
 
     layers, step_ms, eager_ms = headline(args, torch, paged_attention, workloads)
     per_call_ms = step_ms / LAYERS
@@ -346,7 +374,7 @@ def main(argv=None):
     torch.cuda.empty_cache()
     if not args.no_extra:
         result["extra"] = extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention,
-                                          workloads, paged_oracle)
+                                          workloads, paged_oracle, names=tuple(args.extra.split(",")))
         log(f"extra: {json.dumps(result['extra'])}")
     if not args.no_cpu_baseline:
         gen_layers = [workloads.decode_b32_layer(torch.device("cuda:0"), seed=BASE_SEED + 2)]

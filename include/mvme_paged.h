@@ -147,12 +147,24 @@ int mvme_paged_attention(void* out, const void* query,
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Bytes of device workspace mvme_paged_prefill_attention needs for these
+ * shapes (0 when no query block is split over key chunks).  Pure host
+ * function.  chunk_tokens: 0 selects the library's default key chunking.
+ */
+size_t mvme_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
+                                         int64_t kv_heads, int64_t head_dim, int64_t block_size,
+                                         int64_t table_width, int64_t chunk_tokens);
+
+/*
  * Ragged chunked paged prefill: packed queries q[total_tokens, q_heads,
  * head_dim]; sequence s owns rows [cu_seqlens_q[s], cu_seqlens_q[s+1]), whose
  * i-th row sits at absolute position query_starts[s] + i and attends keys
  * [0, query_starts[s] + i] of that sequence through block_tables[s, :]
  * (causal inside the chunk).  context_lens[s] = query_starts[s] + rows(s).
  * Rows whose position is inconsistent with the metadata produce zeros.
+ * Long contexts are split over key chunks of `chunk_tokens` keys (0 = library
+ * default) whose fp32 partials live in `workspace`, which must hold
+ * mvme_paged_prefill_workspace_size(...) bytes (may be NULL when that is 0).
  * Replaces: paged_prefill_attention_cuda / paged_prefill_kernel
  *   (mini_engine/kernels/csrc/prefill.cu:106-240), bound as
  *   extension.paged_prefill_attention (csrc/bindings.cpp:219) and called from
@@ -165,7 +177,8 @@ int mvme_paged_prefill_attention(void* out, const void* q,
                                  int64_t num_seqs, int64_t total_tokens,
                                  int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                                  int64_t num_blocks, int64_t block_size, int64_t table_width,
-                                 int dtype, void* stream);
+                                 int64_t chunk_tokens, int dtype,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -4,34 +4,63 @@
 // [cu[s], cu[s+1]), row i of s sits at absolute position starts[s] + i and
 // attends keys [0, starts[s] + i] of s through its block table.
 //
-// MFMA path (D = 128, G = Hq/Hkv in {1,2,4,8,16}):
-//   One work-group (4 waves) per (sequence, kv head, block of 64/G query
-//   tokens): 64 query rows = (token, head-of-group) pairs that share every
-//   K/V tile.  Wave w owns rows 16w..16w+15.  K/V tiles of 64 keys are
-//   gathered from the pages into LDS (K row-major, V transposed), the next
-//   tile's global loads are in flight while the current tile is multiplied.
+// MFMA path (D = 128, G = Hq/Hkv dividing 256):
+//   Work item = (sequence, kv head, block of 256/G query tokens, chunk of
+//   `chunk` keys).  The 256 query rows of an item = (token, head-of-group)
+//   pairs that share every K/V tile; each of the 8 waves (two per SIMD) owns
+//   32 rows (two 16-row MFMA column blocks).  Long contexts with few query
+//   blocks are cut into key chunks so that the work items spread over all
+//   CUs; items of a query block that needs several chunks write fp32
+//   partials (unnormalised O, running max, running sum) that a merge kernel
+//   combines.  Items are enumerated densely from the metadata on the device,
+//   so grid position i is the i-th real item (work-groups past the end exit).
+//
+//   K/V tiles of 64 keys move from the pages straight into LDS with
+//   global_load_lds_dwordx4 (no VGPR staging) into a ring of 4 stages, the
+//   copies running 3 tiles ahead of the tile being multiplied.  One barrier
+//   per tile both publishes the landed tile and retires the stage the next
+//   copy overwrites.  Each 256-byte key row is stored with its 16-byte
+//   chunks XOR-swizzled by the row index, which keeps both read patterns
+//   below free of bank conflicts.
 //
 //   Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32), so
-//   that each lane ends up holding 16 scores of ONE query row: the online
-//   softmax needs only two cross-lane max exchanges per tile, and the
-//   probabilities are already in the B-operand layout of O^T = V^T P^T
-//   (keys are assigned to MFMA k-slots by a fixed permutation applied to
-//   both operands).  Accumulation, softmax and normalisation are fp32.
+//   each lane holds the scores of ONE query row: the online softmax reduces
+//   across the four k-group lanes with permlane swaps, and the probabilities
+//   already sit in the B-operand layout of O^T = V^T P^T.  The V^T operand
+//   (8 consecutive keys of one dim per lane) is read from the row-major V
+//   tile with two ds_read_b64_tr_b16 transposing loads.  Keys are assigned to
+//   MFMA k-slots by one permutation applied to both operands.  Rescaling of
+//   the accumulators is deferred until a row maximum grows by more than
+//   2^8; tiles that are complete and entirely below the causal diagonal skip
+//   masking.  Accumulation, softmax and normalisation are fp32.
 //
 // Generic path (any D <= 1024, any G): one wave per (query row, head),
 // online softmax over 64-key tiles, fp32 throughout.
 #include "mvme_common.h"
 
+#include <algorithm>
+
 namespace mvme {
 namespace {
 
-constexpr int kPfWaves = 4;
+constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kPfRows = 64;    // query rows per work-group
-constexpr int kPfKeys = 64;    // keys per LDS tile
+constexpr int kPfNb = 2;                        // 16-row MFMA column blocks per wave
+constexpr int kPfRows = kPfWaves * kPfNb * 16;  // 256 query rows per work-group (32 per wave)
+constexpr int kPfStages = 4;                    // LDS ring of K/V tiles
+constexpr int kPfAhead = kPfStages - 1;         // tiles in flight ahead of the one computed
+constexpr int kPfIpw = 16 / kPfWaves;           // 1 KiB copy instructions per wave per K (or V) tile
+constexpr int kPfKeys = 64;        // keys per LDS tile
 constexpr int kPfD = 128;
-constexpr int kKStride = 136;  // K tile row stride in elements (272 B, 16 B aligned)
-constexpr int kVStride = 68;   // V^T tile row stride in elements (136 B = 34 dwords)
+constexpr int kRowBytes = kPfD * 2;             // 256-byte key row
+constexpr int kTileBytes = kPfKeys * kRowBytes;  // 16 KiB per K or V tile
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Finite source for key rows that are absent (out-of-range page, beyond the
+// context): loading zeros keeps every LDS slot finite without predication.
+__device__ __attribute__((aligned(16))) const uint32_t kZeroChunk[4] = {0u, 0u, 0u, 0u};
 
 struct PrefillArgs {
     void* out;
@@ -42,229 +71,532 @@ struct PrefillArgs {
     const int64_t* starts;
     const int64_t* tables;
     const int64_t* lens;
+    float* ws_o;   // [T, Hq, max_chunks, D] unnormalised partial outputs
+    float* ws_ml;  // [T, Hq, max_chunks, 2] (running max in log2 units, sum)
     int num_seqs;
     int q_heads;
     int kv_heads;
     int group;
-    int qb;  // query tokens per work-group (kPfRows / group)
+    int qb;        // query tokens per item (kPfRows / group)
+    int chunk;     // keys per item (multiple of kPfKeys)
+    int max_chunks;
     int head_dim;
     int64_t num_blocks;
     int block_size;
+    int block_shift;  // log2(block_size) when a power of two, else -1
     int table_width;
     float scale_log2;
 };
 
-// Locate (sequence, first query token) of query block `blk`, counting
-// ceil(rows/qb) blocks per sequence in order.  Returns false past the end.
-__device__ inline bool find_block(const PrefillArgs& a, int blk, int& seq, int& q0) {
-    int rem = blk;
-    for (int s = 0; s < a.num_seqs; ++s) {
-        const int64_t n = a.cu[s + 1] - a.cu[s];
-        const int nb = n > 0 ? (int)((n + a.qb - 1) / a.qb) : 0;
-        if (rem < nb) {
-            seq = s;
-            q0 = rem * a.qb;
-            return true;
+// Keys a query block [q0, q0+qb) of sequence s needs: [0, kv_end).
+__device__ inline int64_t block_kv_end(const PrefillArgs& a, int64_t start, int64_t ctx, int64_t qlen, int64_t q0) {
+    const int64_t cap = (int64_t)a.table_width * a.block_size;
+    int64_t e = start + min(q0 + (int64_t)a.qb, qlen);
+    if (e > ctx) e = ctx;
+    if (e > cap) e = cap;
+    return e > 0 ? e : 0;
+}
+
+__device__ inline int chunks_of(const PrefillArgs& a, int64_t kv_end) {
+    return kv_end > 0 ? (int)((kv_end + a.chunk - 1) / a.chunk) : 1;
+}
+
+// Items (query block x key chunk) of sequence s; every query block owns at
+// least one item so its rows always get written.
+__device__ inline int seq_items(const PrefillArgs& a, int s) {
+    const int64_t n = a.cu[s + 1] - a.cu[s];
+    if (n <= 0) return 0;
+    const int64_t start = a.starts[s];
+    const int64_t ctx = a.lens[s];
+    int count = 0;
+    for (int64_t b0 = 0; b0 < n; b0 += a.qb) count += chunks_of(a, block_kv_end(a, start, ctx, n, b0));
+    return count;
+}
+
+// Item `item` -> (sequence, first query token, chunk, kv_end, chunks).
+// Lane-parallel: each lane counts the items of one sequence, a wave prefix
+// sum locates the sequence, then the query blocks of that one sequence are
+// walked.  Every wave of the work-group computes the same answer.
+__device__ inline bool find_item(const PrefillArgs& a, int item, int& seq, int& q0, int& chunk,
+                                 int64_t& kv_end, int& nchunks) {
+    const int lane = __lane_id();
+    int base = 0;
+    for (int s0 = 0; s0 < a.num_seqs; s0 += kWave) {
+        const int s = s0 + lane;
+        const int cnt = s < a.num_seqs ? seq_items(a, s) : 0;
+        int incl = cnt;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int other = __shfl_up(incl, off);
+            if (lane >= off) incl += other;
         }
-        rem -= nb;
+        const int total = __shfl(incl, kWave - 1);
+        if (item < base + total) {
+            const uint64_t hit = __ballot(base + incl > item);
+            const int sel = __builtin_ctzll(hit);
+            seq = s0 + sel;
+            int rem = item - base - (__shfl(incl, sel) - __shfl(cnt, sel));
+            const int64_t n = a.cu[seq + 1] - a.cu[seq];
+            const int64_t start = a.starts[seq];
+            const int64_t ctx = a.lens[seq];
+            for (int64_t b0 = 0; b0 < n; b0 += a.qb) {
+                const int64_t e = block_kv_end(a, start, ctx, n, b0);
+                const int nc = chunks_of(a, e);
+                if (rem < nc) {
+                    q0 = (int)b0;
+                    chunk = rem;
+                    kv_end = e;
+                    nchunks = nc;
+                    return true;
+                }
+                rem -= nc;
+            }
+            return false;  // unreachable when the counts are consistent
+        }
+        base += total;
     }
     return false;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kPfThreads) void paged_prefill_mfma_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) uint16_t sm_k[kPfKeys * kKStride];
-    __shared__ __attribute__((aligned(16))) uint16_t sm_vt[kPfD * kVStride];
-    __shared__ __attribute__((aligned(16))) float sm_bias[kPfKeys];
+// Direct global -> LDS copy of 16 bytes per lane: lane i's bytes land at LDS
+// address `lds_base + 16*i` (lds_base is wave-uniform, passed through M0).
+// Issued as inline assembly so that the compiler does not serialise it
+// against unrelated LDS reads; the kernel orders it with explicit
+// s_waitcnt vmcnt(0) + s_barrier before the destination stage is read.
+// M0 is saved and restored around the copy.
+__device__ inline void lds_dma16(const void* gptr, uint32_t lds_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(gptr), "s"(base));
+}
 
-    int seq, q0;
-    if (!find_block(a, blockIdx.x, seq, q0)) return;
-    const int kvh = blockIdx.y;
+// Wave-wide waits + work-group barrier with a compiler memory fence.
+__device__ inline void dma_landed_barrier() {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+__device__ inline void lds_reads_done_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
+}
+
+template <typename P>
+__device__ inline uint32_t lds_addr(P* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)p;
+}
+
+// LDS byte offset of 16-byte chunk `c` of key row `row` (XOR swizzle).
+__device__ inline int swz(int row, int c) { return row * kRowBytes + 16 * (c ^ (row & 15)); }
+
+// Row rescaling is deferred until a row's running max grows by more than
+// this many binary orders: probabilities stay below 2^kRescaleSlack, far
+// inside fp16/bf16/fp32 range, and the final division by the row sum makes
+// the result independent of the reference max.
+constexpr float kRescaleSlack = 8.f;
+
+// Full wait issued through the builtin, which the compiler's own wait
+// insertion understands (it then knows earlier loads have completed).
+__device__ inline void wait_vmcnt_all() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Max / sum over the four lanes {l, l^16, l^32, l^48} (the 4 MFMA k-groups
+// holding one query row) with gfx950 lane swaps -- no LDS round trip.
+__device__ inline float row4_max(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float row4_sum(float x) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// SCALAR_PAGES: block_size is a multiple of 4, so the 4 key rows one copy
+// instruction covers sit in one page and the page id is wave-uniform (a
+// scalar load).  Then the vector-memory counter only ever holds the tile
+// copies, and "tile t has landed" is exactly vmcnt <= 2 tiles of copies.
+// Otherwise page ids are per-lane vector loads and every tile waits for
+// all outstanding copies (correct, shallower pipeline).
+template <typename T, bool SCALAR_PAGES>
+__global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint8_t sm_k[kPfStages][kTileBytes];
+    __shared__ __attribute__((aligned(16))) uint8_t sm_v[kPfStages][kTileBytes];
+    __shared__ __attribute__((aligned(16))) float sm_b[kPfStages][kPfKeys];
+    __shared__ __attribute__((aligned(16))) int sm_full[kPfStages][kPfWaves];
+
+    int seq, q0, chunk, nchunks;
+    int64_t kv_end64;
+    if (!find_item(a, blockIdx.x / a.kv_heads, seq, q0, chunk, kv_end64, nchunks)) return;
+    // The item is the same for every lane: keep it in scalar registers.
+    seq = __builtin_amdgcn_readfirstlane(seq);
+    q0 = __builtin_amdgcn_readfirstlane(q0);
+    chunk = __builtin_amdgcn_readfirstlane(chunk);
+    nchunks = __builtin_amdgcn_readfirstlane(nchunks);
+    kv_end64 = __builtin_amdgcn_readfirstlane((int)kv_end64);
+    const int kvh = blockIdx.x % a.kv_heads;
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
-    const int li = lane & 15;  // MFMA column / row index
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int li = lane & 15;  // MFMA row / column index
     const int lg = lane >> 4;  // MFMA k-group (0..3)
 
+    // Context positions fit in 31 bits (table capacity <= 2^31 keys).
     const int64_t row0 = a.cu[seq];
     const int qlen = (int)(a.cu[seq + 1] - row0);
-    const int64_t start = a.starts[seq];
+    const int start = (int)a.starts[seq];
     const int64_t ctx = a.lens[seq];
-    const int64_t cap = (int64_t)a.table_width * a.block_size;
+    const int cap = a.table_width * a.block_size;
     const int64_t* table = a.tables + (int64_t)seq * a.table_width;
+    const int kv_end = (int)kv_end64;
+    const int chunk_start = chunk * a.chunk;
+    const int chunk_end = min(chunk_start + a.chunk, kv_end);
+    const int t_begin = chunk_start / kPfKeys;
+    const int t_end = chunk_end > chunk_start ? (chunk_end + kPfKeys - 1) / kPfKeys : t_begin;
 
-    // This lane's query row.
-    const int r = wave * 16 + li;
-    const int qi = q0 + r % a.qb;
-    const int head = kvh * a.group + r / a.qb;
-    const int64_t pos = start + qi;
-    const bool row_ok = qi < qlen && start >= 0 && pos < ctx && pos < cap;
+    // The kPfNb 16-row column blocks of this wave.
+    int qi[kPfNb], head[kPfNb], pos[kPfNb];
+    bool row_ok[kPfNb];
+    int wave_last = -1, wave_first = 0x7fffffff;
+#pragma unroll
+    for (int nb = 0; nb < kPfNb; ++nb) {
+        const int r = wave * (16 * kPfNb) + nb * 16 + li;
+        qi[nb] = q0 + r % a.qb;
+        head[nb] = kvh * a.group + r / a.qb;
+        pos[nb] = start + qi[nb];
+        row_ok[nb] = qi[nb] < qlen && start >= 0 && pos[nb] < ctx && pos[nb] < cap;
+        if (row_ok[nb]) {
+            wave_last = max(wave_last, pos[nb]);
+            wave_first = min(wave_first, pos[nb]);
+        } else {
+            pos[nb] = -1;
+        }
+    }
+#pragma unroll
+    for (int mask = 1; mask < kWave; mask <<= 1) {
+        wave_last = max(wave_last, __shfl_xor(wave_last, mask));
+        wave_first = min(wave_first, __shfl_xor(wave_first, mask));
+    }
+    wave_last = __builtin_amdgcn_readfirstlane(wave_last);
+    wave_first = __builtin_amdgcn_readfirstlane(wave_first);
 
-    // Keys needed by the block: [0, kv_end).
-    const int last_qi = min(q0 + a.qb, qlen) - 1;
-    int64_t kv_end = start + last_qi + 1;
-    if (kv_end > ctx) kv_end = ctx;
-    if (kv_end > cap) kv_end = cap;
-    const int ntiles = kv_end > 0 ? (int)((kv_end + kPfKeys - 1) / kPfKeys) : 0;
-
-    // Q^T operand: lane holds row r, d = 32*dc + 8*lg .. +8.
-    u32x4 qop[4];
-    {
-        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + ((row0 + qi) * a.q_heads + head) * kPfD;
+    // Q^T operands: row (nb, li), d = 32*dc + 8*lg .. +8.  Loaded (and waited
+    // for) before any tile copy is issued, so the copies own the counter.
+    u32x4 qop[kPfNb][4];
+#pragma unroll
+    for (int nb = 0; nb < kPfNb; ++nb) {
+        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + ((row0 + qi[nb]) * a.q_heads + head[nb]) * kPfD;
 #pragma unroll
         for (int dc = 0; dc < 4; ++dc) {
-            qop[dc] = u32x4{0u, 0u, 0u, 0u};
-            if (row_ok) qop[dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
+            qop[nb][dc] = u32x4{0u, 0u, 0u, 0u};
+            if (row_ok[nb]) qop[nb][dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
         }
     }
+    wait_vmcnt_all();
 
-    float m_run = kNegInf, l_part = 0.f;
-    f32x4 o[8];
+    float m_run[kPfNb], l_part[kPfNb];
+    f32x4 o[kPfNb][8];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // Tile loader mapping: load j of lane -> key 16*wave + li, chunk 4*j + lg.
-    const int64_t row_elems = (int64_t)a.kv_heads * kPfD;
-    const uint16_t* kcache = static_cast<const uint16_t*>(a.key_cache) + kvh * kPfD;
-    const uint16_t* vcache = static_cast<const uint16_t*>(a.value_cache) + kvh * kPfD;
-    const int ld_key = 16 * wave + li;
-    u32x4 pk[4], pv[4];
-    bool pvalid = false;
-
-    auto load_tile = [&](int tile) {
-        const int64_t key = (int64_t)tile * kPfKeys + ld_key;
-        int64_t page = -1;
-        if (key < kv_end) page = table[key / a.block_size];
-        pvalid = page >= 0 && page < a.num_blocks;
-        const int64_t off = (page * a.block_size + key % a.block_size) * row_elems;
+    for (int nb = 0; nb < kPfNb; ++nb) {
+        m_run[nb] = kNegInf;
+        l_part[nb] = 0.f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            pk[j] = pv[j] = u32x4{0u, 0u, 0u, 0u};
-            if (pvalid) {
-                pk[j] = *reinterpret_cast<const u32x4*>(kcache + off + 8 * (4 * j + lg));
-                pv[j] = *reinterpret_cast<const u32x4*>(vcache + off + 8 * (4 * j + lg));
-            }
+        for (int dt = 0; dt < 8; ++dt) o[nb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+    // Swizzled LDS offsets this lane reads (independent of the tile):
+    // K chunk 4*dc + lg of row 16*kt + li, and the transposing V reads of
+    // rows 32*c + 4*lg + li/4 (+16), dims 16*dt + 4*(li%4) .. +4.
+    int koff[4];
+#pragma unroll
+    for (int dc = 0; dc < 4; ++dc) koff[dc] = li * kRowBytes + 16 * ((4 * dc + lg) ^ li);
+    const int vrow = 4 * lg + (li >> 2);
+    int voff[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+        voff[dt] = vrow * kRowBytes + 16 * ((2 * dt + ((li & 3) >> 1)) ^ (vrow & 15)) + 8 * (li & 1);
+
+    // Copy plan: a tile's K (and V) is 16 instructions of 1 KiB; wave w issues
+    // instructions j = kPfIpw*w + i, each covering key rows 4j..4j+3 (lane ->
+    // row 4j + lane/16, LDS slot lane%16 = global chunk (lane%16)^(row&15)).
+    const int64_t row_bytes_g = (int64_t)a.kv_heads * kPfD * 2;
+    const int64_t page_bytes_g = (int64_t)a.block_size * row_bytes_g;
+    const uint8_t* kcache = static_cast<const uint8_t*>(a.key_cache) + (int64_t)kvh * kPfD * 2;
+    const uint8_t* vcache = static_cast<const uint8_t*>(a.value_cache) + (int64_t)kvh * kPfD * 2;
+    const int bs_shift = a.block_shift;
+    const int lrow = lane >> 4;  // row inside the instruction's 4 rows
+
+    // The table is read-only here: reading it through the constant address
+    // space lets wave-uniform lookups become scalar loads.
+    typedef __attribute__((address_space(4))) const int64_t const_i64;
+    const const_i64* ctable = (const const_i64*)table;
+    auto page_at = [&](int key) -> int {
+        const int kc = key < cap ? key : cap - 1;
+        const int idx = bs_shift >= 0 ? kc >> bs_shift : kc / a.block_size;
+        const int64_t page = ctable[idx];
+        return (key < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
+    };
+    int pg_next[kPfIpw];  // pages for the next tile to issue
+    auto lookup = [&](int tile) {
+#pragma unroll
+        for (int i = 0; i < kPfIpw; ++i) {
+            const int row = 4 * (kPfIpw * wave + i) + (SCALAR_PAGES ? 0 : lrow);
+            pg_next[i] = page_at(tile * kPfKeys + row);
         }
     };
-
-    auto store_tile = [&]() {
-        // K row-major.
+    auto issue = [&](int tile) {
+        const int st = (tile - t_begin) & (kPfStages - 1);
+        bool all_ok = true;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            *reinterpret_cast<u32x4*>(&sm_k[ld_key * kKStride + 8 * (4 * j + lg)]) = pk[j];
-        // V transposed: lanes li, li^1 hold keys 2m, 2m+1 of the same chunk;
-        // exchange half a chunk so each lane writes (V[2m][d], V[2m+1][d])
-        // dwords for 4 of the chunk's 8 dims.
-        const bool odd = li & 1;
-        const int kpair = ld_key & ~1;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            // Even lane keeps dims 0..3 (dwords 0,1) and sends dwords 2,3.
-            const uint32_t send0 = odd ? pv[j][0] : pv[j][2];
-            const uint32_t send1 = odd ? pv[j][1] : pv[j][3];
-            const uint32_t keep0 = odd ? pv[j][2] : pv[j][0];
-            const uint32_t keep1 = odd ? pv[j][3] : pv[j][1];
-            const uint32_t recv0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send0, kDppQuadSwap1, 0xf, 0xf, false);
-            const uint32_t recv1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)send1, kDppQuadSwap1, 0xf, 0xf, false);
-            // mine/partner words hold dims (2e, 2e+1) of keys kpair+odd / kpair+!odd.
-            const uint32_t e_lo0 = odd ? recv0 : keep0;  // key 2m, dims base+0,1
-            const uint32_t e_lo1 = odd ? recv1 : keep1;  // key 2m, dims base+2,3
-            const uint32_t e_hi0 = odd ? keep0 : recv0;  // key 2m+1, dims base+0,1
-            const uint32_t e_hi1 = odd ? keep1 : recv1;  // key 2m+1, dims base+2,3
-            const int dbase = 8 * (4 * j + lg) + (odd ? 4 : 0);
-            const uint32_t w0 = (e_lo0 & 0xffffu) | (e_hi0 << 16);
-            const uint32_t w1 = (e_lo0 >> 16) | (e_hi0 & 0xffff0000u);
-            const uint32_t w2 = (e_lo1 & 0xffffu) | (e_hi1 << 16);
-            const uint32_t w3 = (e_lo1 >> 16) | (e_hi1 & 0xffff0000u);
-            *reinterpret_cast<uint32_t*>(&sm_vt[(dbase + 0) * kVStride + kpair]) = w0;
-            *reinterpret_cast<uint32_t*>(&sm_vt[(dbase + 1) * kVStride + kpair]) = w1;
-            *reinterpret_cast<uint32_t*>(&sm_vt[(dbase + 2) * kVStride + kpair]) = w2;
-            *reinterpret_cast<uint32_t*>(&sm_vt[(dbase + 3) * kVStride + kpair]) = w3;
+        for (int i = 0; i < kPfIpw; ++i) {
+            const int j = kPfIpw * wave + i;
+            const int row = 4 * j + lrow;
+            const int key = tile * kPfKeys + row;
+            const int cidx = (lane & 15) ^ (row & 15);
+            const int page = pg_next[i];
+            // Rows past the chunk inside a valid first-row page are masked too.
+            const bool ok = page >= 0 && key < chunk_end;
+            all_ok = all_ok && ok;
+            const uint8_t* gk = reinterpret_cast<const uint8_t*>(kZeroChunk);
+            const uint8_t* gv = gk;
+            if (ok) {
+                const int in_page = bs_shift >= 0 ? key & (a.block_size - 1) : key % a.block_size;
+                const int64_t off = (int64_t)page * page_bytes_g + (int64_t)in_page * row_bytes_g + 16 * cidx;
+                gk = kcache + off;
+                gv = vcache + off;
+            }
+            lds_dma16(gk, lds_addr(&sm_k[st][0]) + 1024 * j);
+            lds_dma16(gv, lds_addr(&sm_v[st][0]) + 1024 * j);
+            if ((lane & 15) == 0) sm_b[st][row] = ok ? 0.f : kNegInf;
         }
-        if (lg == 0) sm_bias[ld_key] = pvalid ? 0.f : kNegInf;
+        const bool wave_full = __builtin_amdgcn_ballot_w64(!all_ok) == 0;
+        if (lane == 0) sm_full[st][wave] = wave_full ? 1 : 0;
     };
 
-    if (ntiles > 0) load_tile(0);
-    for (int tile = 0; tile < ntiles; ++tile) {
-        __syncthreads();  // previous tile fully consumed
-        store_tile();
-        __syncthreads();
-        if (tile + 1 < ntiles) load_tile(tile + 1);
-
-        // S^T = K Q^T for the 4 key sub-tiles of 16.
-        f32x4 s[4];
+    // Prologue: tiles t_begin .. t_begin+kPfAhead-1 in flight (copies of
+    // tiles past the chunk read zeros into stages nobody computes on, which
+    // keeps the per-iteration copy count constant).
+    if (t_begin < t_end) {
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < kPfAhead; ++k) {
+            lookup(t_begin + k);
+            issue(t_begin + k);
+        }
+        lookup(t_begin + kPfAhead);
+    }
+    for (int tile = t_begin; tile < t_end; ++tile) {
+        const int st = (tile - t_begin) & (kPfStages - 1);
+        // Tile `tile` has landed for this lane when at most the copies of the
+        // later tiles in flight are outstanding; the barrier makes every
+        // lane's copies visible.  It also proves every wave has finished (and
+        // received all LDS reads of) the previous tile, whose stage the copy
+        // below refills (a ring of kPfStages stages with copies kPfStages-1
+        // tiles ahead): one barrier per tile.
+        if constexpr (SCALAR_PAGES) {
+            static_assert(2 * kPfIpw * (kPfAhead - 1) == 8, "vmcnt immediate below");
+            asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" : : : "memory");
+        } else {
+            dma_landed_barrier();
+        }
+        issue(tile + kPfAhead);
+        lookup(tile + kPfAhead + 1);
+        const int tile0 = tile * kPfKeys;
+        if (tile0 <= wave_last) {
+            const uint8_t* smk = &sm_k[st][0];
+            const float* smb = &sm_b[st][0];
+            // Every key of the tile present and visible to every row of the
+            // wave: no bias and no causal mask needed.
+            static_assert(kPfWaves == 8, "two int4 flag reads below");
+            const int4 fa = *reinterpret_cast<const int4*>(&sm_full[st][0]);
+            const int4 fb = *reinterpret_cast<const int4*>(&sm_full[st][4]);
+            const bool fast = (fa.x & fa.y & fa.z & fa.w & fb.x & fb.y & fb.z & fb.w) &&
+                              tile0 + kPfKeys - 1 <= wave_first;
+            typedef __attribute__((address_space(3))) uint8_t lds_u8;
+            lds_u8* vbase = (lds_u8*)&sm_v[st][0];
+            // Two halves of 32 keys: S^T -> softmax -> O^T += V^T P^T each.
 #pragma unroll
-            for (int dc = 0; dc < 4; ++dc) {
-                const u32x4 kop = *reinterpret_cast<const u32x4*>(&sm_k[(16 * kt + li) * kKStride + 32 * dc + 8 * lg]);
-                s[kt] = T::mfma16x16x32(kop, qop[dc], s[kt]);
+            for (int h = 0; h < 2; ++h) {
+                // S^T = K Q^T for key sub-tiles 2h, 2h+1: 8 independent accumulators.
+                f32x4 sc[kPfNb][2];
+#pragma unroll
+                for (int nb = 0; nb < kPfNb; ++nb) sc[nb][0] = sc[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int dc = 0; dc < 4; ++dc) {
+                    const u32x4 k0 = *reinterpret_cast<const u32x4*>(smk + 32 * h * kRowBytes + koff[dc]);
+                    const u32x4 k1 = *reinterpret_cast<const u32x4*>(smk + (32 * h + 16) * kRowBytes + koff[dc]);
+#pragma unroll
+                    for (int nb = 0; nb < kPfNb; ++nb) {
+                        sc[nb][0] = T::mfma16x16x32(k0, qop[nb][dc], sc[nb][0]);
+                        sc[nb][1] = T::mfma16x16x32(k1, qop[nb][dc], sc[nb][1]);
+                    }
+                }
+                // Row maxima over the 32 keys (log2 units).
+                float mx[kPfNb];
+                if (fast) {
+#pragma unroll
+                    for (int nb = 0; nb < kPfNb; ++nb) {
+                        float r = sc[nb][0][0];
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) r = fmaxf(r, sc[nb][kk][j]);
+                        mx[nb] = row4_max(r) * a.scale_log2;
+                    }
+                } else {
+#pragma unroll
+                    for (int nb = 0; nb < kPfNb; ++nb) {
+                        const int lim = pos[nb] - tile0 - 32 * h - 4 * lg;  // key (16*kk + j) must be <= lim
+                        float r = kNegInf;
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk) {
+                            const f32x4 bias = *reinterpret_cast<const f32x4*>(&smb[32 * h + 16 * kk + 4 * lg]);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) {
+                                float v = sc[nb][kk][j] * a.scale_log2 + bias[j];
+                                if (16 * kk + j > lim) v = kNegInf;
+                                sc[nb][kk][j] = v;
+                                r = fmaxf(r, v);
+                            }
+                        }
+                        mx[nb] = row4_max(r);
+                    }
+                }
+                // Deferred rescale: only when some row's max outgrew its reference.
+                bool grow = false;
+#pragma unroll
+                for (int nb = 0; nb < kPfNb; ++nb) grow = grow || mx[nb] > m_run[nb] + kRescaleSlack;
+                if (__builtin_amdgcn_ballot_w64(grow)) {
+#pragma unroll
+                    for (int nb = 0; nb < kPfNb; ++nb) {
+                        const float mn = fmaxf(m_run[nb], mx[nb]);
+                        const float alpha = mn == kNegInf ? 1.f : fast_exp2(m_run[nb] - mn);
+                        m_run[nb] = mn;
+                        l_part[nb] *= alpha;
+#pragma unroll
+                        for (int dt = 0; dt < 8; ++dt) o[nb][dt] *= alpha;
+                    }
+                }
+                // Probabilities, packed as the B operand of the PV products:
+                // k-slot 4*kk + j <-> key 32h + 16kk + 4*lg + j.
+                u32x4 pop[kPfNb];
+                if (fast) {
+#pragma unroll
+                    for (int nb = 0; nb < kPfNb; ++nb) {
+                        const float nref = m_run[nb] == kNegInf ? 0.f : -m_run[nb];
+                        float p[8];
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) p[4 * kk + j] = fast_exp2(fmaf(sc[nb][kk][j], a.scale_log2, nref));
+                        l_part[nb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                        pop[nb] = u32x4{T::pack(p[0], p[1]), T::pack(p[2], p[3]), T::pack(p[4], p[5]),
+                                        T::pack(p[6], p[7])};
+                    }
+                } else {
+#pragma unroll
+                    for (int nb = 0; nb < kPfNb; ++nb) {
+                        const float ref = m_run[nb] == kNegInf ? 0.f : m_run[nb];
+                        float p[8];
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) p[4 * kk + j] = fast_exp2(sc[nb][kk][j] - ref);
+                        l_part[nb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+                        pop[nb] = u32x4{T::pack(p[0], p[1]), T::pack(p[2], p[3]), T::pack(p[4], p[5]),
+                                        T::pack(p[6], p[7])};
+                    }
+                }
+                // O^T += V^T P^T for these 32 keys; V^T operand by transposing reads.
+#pragma unroll
+                for (int dt = 0; dt < 8; ++dt) {
+                    const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(vbase + 32 * h * kRowBytes + voff[dt]));
+                    const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(vbase + (32 * h + 16) * kRowBytes + voff[dt]));
+                    const u32x2 w0 = __builtin_bit_cast(u32x2, t0);
+                    const u32x2 w1 = __builtin_bit_cast(u32x2, t1);
+                    const u32x4 vop = {w0[0], w0[1], w1[0], w1[1]};
+#pragma unroll
+                    for (int nb = 0; nb < kPfNb; ++nb) o[nb][dt] = T::mfma16x16x32(vop, pop[nb], o[nb][dt]);
+                }
             }
         }
+    }
+    // Drain the trailing copies before the work-group's LDS can be reassigned.
+    wait_vmcnt_all();
 
-        // Online softmax for this lane's row over its 16 keys.
-        const int64_t tile0 = (int64_t)tile * kPfKeys;
-        float mx = kNegInf;
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            const f32x4 bias = *reinterpret_cast<const f32x4*>(&sm_bias[16 * kt + 4 * lg]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int64_t key = tile0 + 16 * kt + 4 * lg + j;
-                float v = s[kt][j] * a.scale_log2 + bias[j];
-                if (!row_ok || key > pos) v = kNegInf;
-                s[kt][j] = v;
-                mx = fmaxf(mx, v);
-            }
-        }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
-        const float mn = fmaxf(m_run, mx);
-        const float ref = mn == kNegInf ? 0.f : mn;
-        const float alpha = fast_exp2(m_run - ref);
-        m_run = mn;
-        float psum = 0.f;
-        uint32_t pp[8];
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt) {
-            float p[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                p[j] = fast_exp2(s[kt][j] - ref);
-                psum += p[j];
-            }
-            pp[2 * kt] = T::pack(p[0], p[1]);
-            pp[2 * kt + 1] = T::pack(p[2], p[3]);
-        }
-        l_part = l_part * alpha + psum;
-#pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
-
-        // O^T += V^T P^T over two 32-key chunks.
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            const u32x4 pop = {pp[4 * c], pp[4 * c + 1], pp[4 * c + 2], pp[4 * c + 3]};
+    for (int nb = 0; nb < kPfNb; ++nb) {
+        const float l_row = row4_sum(l_part[nb]);
+        if (qi[nb] >= qlen) continue;
+        const int64_t rowid = (row0 + qi[nb]) * a.q_heads + head[nb];
+        if (nchunks == 1) {
+            const float inv = (row_ok[nb] && l_row > 0.f) ? 1.f / l_row : 0.f;
+            uint16_t* orow = static_cast<uint16_t*>(a.out) + rowid * kPfD;
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
-                const uint16_t* vrow = &sm_vt[(16 * dt + li) * kVStride + 32 * c + 4 * lg];
-                const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-                const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
-                const u32x4 vop = {lo[0], lo[1], hi[0], hi[1]};
-                o[dt] = T::mfma16x16x32(vop, pop, o[dt]);
+                const u32x2 w = {T::pack(o[nb][dt][0] * inv, o[nb][dt][1] * inv),
+                                 T::pack(o[nb][dt][2] * inv, o[nb][dt][3] * inv)};
+                *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * lg) = w;
+            }
+        } else {
+            const int64_t slot = rowid * a.max_chunks + chunk;
+            float* po = a.ws_o + slot * kPfD;
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lg) = o[nb][dt];
+            if (lg == 0) {
+                a.ws_ml[slot * 2] = row_ok[nb] ? m_run[nb] : kNegInf;
+                a.ws_ml[slot * 2 + 1] = row_ok[nb] ? l_row : 0.f;
             }
         }
     }
+}
 
-    // Row sum across the four k-groups holding this row's keys.
-    float l_row = l_part + shfl_xor(l_part, 16);
-    l_row += shfl_xor(l_row, 32);
-    if (qi >= qlen) return;
-    const float inv = (row_ok && l_row > 0.f) ? 1.f / l_row : 0.f;
-    uint16_t* orow = static_cast<uint16_t*>(a.out) + ((row0 + qi) * a.q_heads + head) * kPfD;
+// Combines the key-chunk partials of rows whose query block needed several
+// chunks: out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
+// One work-group per packed token (the sequence lookup happens once for all
+// heads); thread t handles head t/16, dims 8*(t%16) .. +8.
+constexpr int kMergeThreads = 256;
+
+template <typename T>
+__global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(PrefillArgs a) {
+    const int64_t token = blockIdx.x;
+    int lo = 0, hi = a.num_seqs;
+    while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        if (a.cu[mid + 1] <= token) lo = mid + 1;
+        else hi = mid;
+    }
+    if (lo >= a.num_seqs || token < a.cu[lo]) return;
+    const int64_t n = a.cu[lo + 1] - a.cu[lo];
+    const int64_t qi = token - a.cu[lo];
+    const int64_t b0 = qi / a.qb * a.qb;
+    const int nchunks = chunks_of(a, block_kv_end(a, a.starts[lo], a.lens[lo], n, b0));
+    if (nchunks <= 1) return;
+    for (int idx = threadIdx.x; idx < a.q_heads * (kPfD / 8); idx += kMergeThreads) {
+        const int head = idx / (kPfD / 8);
+        const int d0 = 8 * (idx % (kPfD / 8));
+        const int64_t slot0 = (token * a.q_heads + head) * a.max_chunks;
+        const float* ml = a.ws_ml + slot0 * 2;
+        float mx = kNegInf;
+        for (int c = 0; c < nchunks; ++c) mx = fmaxf(mx, ml[2 * c]);
+        const float ref = mx == kNegInf ? 0.f : mx;
+        float sum = 0.f;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int c = 0; c < nchunks; ++c) {
+            const float w = fast_exp2(ml[2 * c] - ref);
+            sum += ml[2 * c + 1] * w;
+            const f32x4* po = reinterpret_cast<const f32x4*>(a.ws_o + (slot0 + c) * kPfD + d0);
+            const f32x4 x0 = po[0], x1 = po[1];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-        const u32x2 w = {T::pack(o[dt][0] * inv, o[dt][1] * inv), T::pack(o[dt][2] * inv, o[dt][3] * inv)};
-        *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * lg) = w;
+            for (int i = 0; i < 4; ++i) {
+                acc[i] = fmaf(x0[i], w, acc[i]);
+                acc[4 + i] = fmaf(x1[i], w, acc[4 + i]);
+            }
+        }
+        const float inv = sum > 0.f ? 1.f / sum : 0.f;
+        const u32x4 wv = {T::pack(acc[0] * inv, acc[1] * inv), T::pack(acc[2] * inv, acc[3] * inv),
+                          T::pack(acc[4] * inv, acc[5] * inv), T::pack(acc[6] * inv, acc[7] * inv)};
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + (token * a.q_heads + head) * kPfD + d0) = wv;
     }
 }
 
@@ -388,10 +720,59 @@ int check_prefill(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64
     return MVME_OK;
 }
 
+struct PrefillPlan {
+    bool mfma;
+    int qb;
+    int chunk;
+    int max_chunks;
+    int64_t items_bound;
+};
+
+constexpr int64_t kPrefillCUs = 256;
+
+// Host plan from shapes only (lengths stay on the device).  Enough query
+// blocks to occupy the GPU twice over: no key split.  Otherwise split the
+// keys into chunks of at least 512 (and at most 16 chunks per block), which
+// spreads long contexts over all CUs at the cost of fp32 partials.
+PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64_t kv_heads,
+                              int64_t head_dim, int64_t block_size, int64_t table_width, int64_t chunk_tokens) {
+    PrefillPlan p{};
+    const int64_t group = q_heads / kv_heads;
+    p.mfma = head_dim == kPfD && kPfRows % group == 0;
+    if (!p.mfma) return p;
+    p.qb = (int)(kPfRows / group);
+    const int64_t cap = table_width * block_size;
+    const int64_t cap_tiles = (cap + kPfKeys - 1) / kPfKeys * kPfKeys;
+    const int64_t blocks_bound = (total_tokens + p.qb - 1) / p.qb + num_seqs;
+    int64_t chunk;
+    if (chunk_tokens > 0) chunk = (chunk_tokens + kPfKeys - 1) / kPfKeys * kPfKeys;
+    else if (blocks_bound * kv_heads >= kPrefillCUs + kPrefillCUs / 2) chunk = cap_tiles;
+    else chunk = std::max<int64_t>(512, ((cap + 15) / 16 + kPfKeys - 1) / kPfKeys * kPfKeys);
+    if (chunk > cap_tiles) chunk = cap_tiles;
+    if (chunk < kPfKeys) chunk = kPfKeys;
+    p.chunk = (int)chunk;
+    p.max_chunks = (int)((cap + chunk - 1) / chunk);
+    if (p.max_chunks < 1) p.max_chunks = 1;
+    p.items_bound = blocks_bound * p.max_chunks;
+    return p;
+}
+
 }  // namespace
 }  // namespace mvme
 
 using namespace mvme;
+
+extern "C" size_t mvme_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
+                                                    int64_t kv_heads, int64_t head_dim, int64_t block_size,
+                                                    int64_t table_width, int64_t chunk_tokens) {
+    if (num_seqs <= 0 || total_tokens <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 ||
+        block_size <= 0 || table_width <= 0)
+        return 0;
+    const PrefillPlan p = make_prefill_plan(num_seqs, total_tokens, q_heads, kv_heads, head_dim, block_size,
+                                            table_width, chunk_tokens);
+    if (!p.mfma || p.max_chunks <= 1) return 0;
+    return (size_t)total_tokens * q_heads * p.max_chunks * (kPfD + 2) * sizeof(float);
+}
 
 extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void* key_cache,
                                             const void* value_cache, const int64_t* cu_seqlens_q,
@@ -399,7 +780,8 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
                                             const int64_t* context_lens, int64_t num_seqs,
                                             int64_t total_tokens, int64_t q_heads, int64_t kv_heads,
                                             int64_t head_dim, int64_t num_blocks, int64_t block_size,
-                                            int64_t table_width, int dtype, void* stream) {
+                                            int64_t table_width, int64_t chunk_tokens, int dtype,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
     if (int rc = check_prefill(num_seqs, total_tokens, q_heads, kv_heads, head_dim, num_blocks,
                                block_size, table_width, dtype))
         return rc;
@@ -408,6 +790,13 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
     if (!out || !q || !key_cache || !value_cache || !cu_seqlens_q || !query_starts || !block_tables ||
         !context_lens)
         return fail(MVME_EINVAL, "paged prefill received a null pointer");
+    const size_t need = mvme_paged_prefill_workspace_size(num_seqs, total_tokens, q_heads, kv_heads, head_dim,
+                                                          block_size, table_width, chunk_tokens);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(MVME_EWORKSPACE, "paged prefill workspace too small: need " + std::to_string(need) +
+                                         " bytes, got " + std::to_string(workspace_bytes));
+    const PrefillPlan p = make_prefill_plan(num_seqs, total_tokens, q_heads, kv_heads, head_dim, block_size,
+                                            table_width, chunk_tokens);
     PrefillArgs a{};
     a.out = out;
     a.q = q;
@@ -424,19 +813,38 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
     a.head_dim = (int)head_dim;
     a.num_blocks = num_blocks;
     a.block_size = (int)block_size;
+    a.block_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctzll((unsigned long long)block_size) : -1;
     a.table_width = (int)table_width;
     a.scale_log2 = kLog2e / sqrtf((float)head_dim);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const bool mfma = head_dim == kPfD && kPfRows % a.group == 0 && a.group <= 16;
-    if (mfma) {
-        a.qb = kPfRows / a.group;
-        const int64_t blocks = (total_tokens + a.qb - 1) / a.qb + num_seqs;
-        if (blocks > 2147483647 || kv_heads > 65535) return fail(MVME_EINVAL, "paged prefill grid too large");
-        const dim3 grid((unsigned)blocks, (unsigned)kv_heads);
-        if (dtype == MVME_FP16)
-            hipLaunchKernelGGL((paged_prefill_mfma_kernel<Half>), grid, dim3(kPfThreads), 0, s, a);
-        else
-            hipLaunchKernelGGL((paged_prefill_mfma_kernel<BFloat16>), grid, dim3(kPfThreads), 0, s, a);
+    if (p.mfma) {
+        if (table_width * block_size > 2147483647)
+            return fail(MVME_EINVAL, "paged prefill table capacity exceeds 2^31 tokens");
+        a.qb = p.qb;
+        a.chunk = p.chunk;
+        a.max_chunks = p.max_chunks;
+        if (need > 0) {
+            a.ws_o = static_cast<float*>(workspace);
+            a.ws_ml = a.ws_o + total_tokens * q_heads * p.max_chunks * kPfD;
+        }
+        const int64_t groups = p.items_bound * kv_heads;
+        if (groups > 2147483647) return fail(MVME_EINVAL, "paged prefill grid too large");
+        const bool scalar_pages = block_size % 4 == 0;
+        const dim3 grid((unsigned)groups), block(kPfThreads);
+        if (dtype == MVME_FP16) {
+            if (scalar_pages) hipLaunchKernelGGL((paged_prefill_mfma_kernel<Half, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((paged_prefill_mfma_kernel<Half, false>), grid, block, 0, s, a);
+        } else {
+            if (scalar_pages) hipLaunchKernelGGL((paged_prefill_mfma_kernel<BFloat16, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((paged_prefill_mfma_kernel<BFloat16, false>), grid, block, 0, s, a);
+        }
+        if (p.max_chunks > 1) {
+            const dim3 grid((unsigned)total_tokens);
+            if (dtype == MVME_FP16)
+                hipLaunchKernelGGL((paged_prefill_merge_kernel<Half>), grid, dim3(kMergeThreads), 0, s, a);
+            else
+                hipLaunchKernelGGL((paged_prefill_merge_kernel<BFloat16>), grid, dim3(kMergeThreads), 0, s, a);
+        }
     } else {
         if (q_heads > 65535) return fail(MVME_EINVAL, "paged prefill grid too large");
         const dim3 grid((unsigned)total_tokens, (unsigned)q_heads);

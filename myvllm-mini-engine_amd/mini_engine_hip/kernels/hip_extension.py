@@ -35,8 +35,9 @@ SIGNATURES = {
     "mvme_paged_attention_workspace_size": (_size, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "mvme_paged_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                     _i64, _i64, _int, _vp, _size, _vp]),
+    "mvme_paged_prefill_workspace_size": (_size, [_i64] * 8),
     "mvme_paged_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
-                                            _i64, _i64, _i64, _i64, _i64, _int, _vp]),
+                                            _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _size, _vp]),
 }
 
 
@@ -65,6 +66,9 @@ class HipLibrary:
 
     def workspace_size(self, *args) -> int:
         return int(self._lib.mvme_paged_attention_workspace_size(*args))
+
+    def prefill_workspace_size(self, *args) -> int:
+        return int(self._lib.mvme_paged_prefill_workspace_size(*args))
 
 
 @functools.lru_cache(maxsize=1)

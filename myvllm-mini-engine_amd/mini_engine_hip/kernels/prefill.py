@@ -17,13 +17,17 @@ MAX_HEAD_DIM = 1024
 
 
 def paged_prefill_attention(q, key_cache, value_cache, cu_seqlens_q, query_starts,
-                            block_tables, context_lens, block_size, *, backend="hip", validate=True):
+                            block_tables, context_lens, block_size, *, backend="hip", validate=True,
+                            chunk_tokens=0, workspace=None):
     """Packed causal queries read paged KV directly.
 
     Q is [total_queries, query_heads, head_dim].  Each request describes a
     suffix starting at its absolute query_start; context_len equals
     start + query_count.  Validation of metadata values synchronizes the
     device; trusted model batches can skip it.
+
+    ``chunk_tokens`` (0 = library default) sets the key-chunk length used to
+    split long contexts; ``workspace`` may supply the partial-result buffer.
     """
     if backend != "hip":
         raise ValueError("paged prefill backend must be hip")
@@ -70,10 +74,17 @@ def paged_prefill_attention(q, key_cache, value_cache, cu_seqlens_q, query_start
         return output
     lib = ext.load_hip_extension()
     num_blocks, _, kv_heads, head_dim = key_cache.shape
+    num_seqs, width = query_starts.numel(), block_tables.shape[1]
+    need = lib.prefill_workspace_size(num_seqs, q.shape[0], q.shape[1], kv_heads, head_dim, block_size, width,
+                                      chunk_tokens)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else 0
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     with torch.cuda.device(q.device):
         lib.call("mvme_paged_prefill_attention", output.data_ptr(), q.data_ptr(), key_cache.data_ptr(),
                  value_cache.data_ptr(), cu_seqlens_q.data_ptr(), query_starts.data_ptr(),
-                 block_tables.data_ptr(), context_lens.data_ptr(), query_starts.numel(), q.shape[0],
-                 q.shape[1], kv_heads, head_dim, num_blocks, block_size, block_tables.shape[1],
-                 ext.dtype_code(q.dtype), ext.current_stream(q.device))
+                 block_tables.data_ptr(), context_lens.data_ptr(), num_seqs, q.shape[0],
+                 q.shape[1], kv_heads, head_dim, num_blocks, block_size, width, chunk_tokens,
+                 ext.dtype_code(q.dtype), ws_ptr, ws_bytes, ext.current_stream(q.device))
     return output

@@ -30,7 +30,7 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     symbols = declared_symbols()
-    assert len(symbols) == 9
+    assert len(symbols) == 10
     raw = ctypes.CDLL(str(hip_build.library_path()))
     for name in symbols:
         assert hasattr(raw, name), name
@@ -82,14 +82,21 @@ def test_scatter_and_prefill_reject_bad_arguments(lib):
     assert "stride" in lib.last_error()
     assert _status(lib, "mvme_write_kv_cache", 1, 1, 4, 16, 8, 128, 1, 2, 30, 1, 1, 5, 1, None) == ext.EINVAL
     assert "exceeds" in lib.last_error()
-    assert _status(lib, "mvme_paged_prefill_attention", 1, 1, 1, 1, 1, 1, 1, 1, 1, 4, 16, 8, 2048, 4, 16, 1, 0,
-                   None) == ext.EINVAL
+    assert _status(lib, "mvme_paged_prefill_attention", 1, 1, 1, 1, 1, 1, 1, 1, 1, 4, 16, 8, 2048, 4, 16, 1, 0, 0,
+                   None, 0, None) == ext.EINVAL
     assert "1024" in lib.last_error()
+    # Few query blocks + long table: key-chunk split needs a workspace.
+    need = lib.prefill_workspace_size(8, 1024, 16, 8, 128, 256, 16, 0)
+    assert need == 1024 * 16 * 8 * (128 + 2) * 4
+    assert _status(lib, "mvme_paged_prefill_attention", 1, 1, 1, 1, 1, 1, 1, 1, 8, 1024, 16, 8, 128, 200, 256, 16,
+                   0, 0, None, 0, None) == ext.EWORKSPACE
+    # Many query blocks: no split, no workspace.
+    assert lib.prefill_workspace_size(8, 1 << 16, 16, 8, 128, 256, 16, 0) == 0
     # Empty inputs are legal no-ops.
     assert _status(lib, "mvme_write_kv_cache_slots", 1, 1, 4, 16, 8, 128, None, None, None, 0, 1024, 1024, 1,
                    None) == ext.OK
     assert _status(lib, "mvme_paged_prefill_attention", None, None, None, None, None, None, None, None, 0, 0, 16, 8,
-                   128, 4, 16, 0, 1, None) == ext.OK
+                   128, 4, 16, 0, 0, 1, None, 0, None) == ext.OK
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
