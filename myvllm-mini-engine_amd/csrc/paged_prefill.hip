@@ -212,14 +212,39 @@ __device__ inline float row4_sum(float x) {
     return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Direct global -> LDS copy from a wave-uniform base plus a per-lane 32-bit
+// byte offset (the SGPR-base form of global_load_lds_dwordx4: no 64-bit
+// per-lane address arithmetic).
+__device__ inline void lds_dma16_s(const uint8_t* sbase, uint32_t voff, uint32_t lds_base) {
+    const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
+    const uint64_t g = (uint64_t)(uintptr_t)sbase;
+    const uint64_t gu = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(g >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)g);
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved) : "v"(voff), "s"(gu), "s"(base));
+}
+
+constexpr int kPagesPerLane = 0;
+constexpr int kPagesPerRows = 1;
+constexpr int kPagesPerTile = 2;
+
+// How page ids are found (PAGES):
+//   kPagesPerTile: block_size is a power of two >= 64, so a 64-key tile lies
+//     in one page: one scalar page lookup per tile, and a full tile's copies
+//     are a scalar base plus precomputed per-lane offsets -- a few scalar
+//     instructions per tile, which matters because the scalar unit is shared
+//     by all waves of the CU.
+//   kPagesPerRows: see below; the fallback for partial tiles as well.
 // SCALAR_PAGES: block_size is a multiple of 4, so the 4 key rows one copy
 // instruction covers sit in one page and the page id is wave-uniform (a
 // scalar load).  Then the vector-memory counter only ever holds the tile
 // copies, and "tile t has landed" is exactly vmcnt <= 2 tiles of copies.
 // Otherwise page ids are per-lane vector loads and every tile waits for
 // all outstanding copies (correct, shallower pipeline).
-template <typename T, bool SCALAR_PAGES>
+template <typename T, int PAGES>
 __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(PrefillArgs a) {
+    constexpr bool SCALAR_PAGES = PAGES != kPagesPerLane;
     __shared__ __attribute__((aligned(16))) uint8_t sm_k[kPfStages][kTileBytes];
     __shared__ __attribute__((aligned(16))) uint8_t sm_v[kPfStages][kTileBytes];
     __shared__ __attribute__((aligned(16))) float sm_b[kPfStages][kPfKeys];
@@ -324,6 +349,12 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
     const uint8_t* vcache = static_cast<const uint8_t*>(a.value_cache) + (int64_t)kvh * kPfD * 2;
     const int bs_shift = a.block_shift;
     const int lrow = lane >> 4;  // row inside the instruction's 4 rows
+    uint32_t tile_off[kPfIpw];   // per-lane byte offset of a whole-tile copy from the tile's row 0
+#pragma unroll
+    for (int i = 0; i < kPfIpw; ++i) {
+        const int row = 4 * (kPfIpw * wave + i) + lrow;
+        tile_off[i] = (uint32_t)(row * row_bytes_g) + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+    }
 
     // The table is read-only here: reading it through the constant address
     // space lets wave-uniform lookups become scalar loads.
@@ -337,14 +368,40 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
     };
     int pg_next[kPfIpw];  // pages for the next tile to issue
     auto lookup = [&](int tile) {
+        if constexpr (PAGES == kPagesPerTile) {
+            // The whole tile lies in one page (-1 when absent or past the chunk).
+            const int key0 = tile * kPfKeys;
+            const int64_t page = ctable[(key0 < cap ? key0 : cap - 1) >> bs_shift];
+            const int pg = (key0 < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
 #pragma unroll
-        for (int i = 0; i < kPfIpw; ++i) {
-            const int row = 4 * (kPfIpw * wave + i) + (SCALAR_PAGES ? 0 : lrow);
-            pg_next[i] = page_at(tile * kPfKeys + row);
+            for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pg;
+        } else {
+#pragma unroll
+            for (int i = 0; i < kPfIpw; ++i) {
+                const int row = 4 * (kPfIpw * wave + i) + (SCALAR_PAGES ? 0 : lrow);
+                pg_next[i] = page_at(tile * kPfKeys + row);
+            }
         }
     };
-    auto issue = [&](int tile) {
-        const int st = (tile - t_begin) & (kPfStages - 1);
+    auto issue = [&](int tile, int st) {
+        if constexpr (PAGES == kPagesPerTile) {
+            const int key0 = tile * kPfKeys;
+            if (pg_next[0] >= 0 && key0 + kPfKeys - 1 < chunk_end) {
+                // Full tile in one page: one scalar base for all copies.
+                const int64_t base =
+                    (int64_t)pg_next[0] * page_bytes_g + (int64_t)(key0 & (a.block_size - 1)) * row_bytes_g;
+                const uint32_t lk = lds_addr(&sm_k[st][0]), lv = lds_addr(&sm_v[st][0]);
+#pragma unroll
+                for (int i = 0; i < kPfIpw; ++i) {
+                    const int j = kPfIpw * wave + i;
+                    lds_dma16_s(kcache + base, tile_off[i], lk + 1024 * j);
+                    lds_dma16_s(vcache + base, tile_off[i], lv + 1024 * j);
+                    if ((lane & 15) == 0) sm_b[st][4 * j + lrow] = 0.f;
+                }
+                if (lane == 0) sm_full[st][wave] = 1;
+                return;
+            }
+        }
         bool all_ok = true;
 #pragma unroll
         for (int i = 0; i < kPfIpw; ++i) {
@@ -379,12 +436,13 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
 #pragma unroll
         for (int k = 0; k < kPfAhead; ++k) {
             lookup(t_begin + k);
-            issue(t_begin + k);
+            issue(t_begin + k, k);
         }
         lookup(t_begin + kPfAhead);
     }
+    int st = kPfStages - 1;  // ring position of `tile` (advanced at the top of the loop)
     for (int tile = t_begin; tile < t_end; ++tile) {
-        const int st = (tile - t_begin) & (kPfStages - 1);
+        st = (st + 1) & (kPfStages - 1);
         // Tile `tile` has landed for this lane when at most the copies of the
         // later tiles in flight are outstanding; the barrier makes every
         // lane's copies visible.  It also proves every wave has finished (and
@@ -397,7 +455,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
         } else {
             dma_landed_barrier();
         }
-        issue(tile + kPfAhead);
+        issue(tile + kPfAhead, (st + kPfAhead) & (kPfStages - 1));
         lookup(tile + kPfAhead + 1);
         const int tile0 = tile * kPfKeys;
         if (tile0 <= wave_last) {
@@ -829,14 +887,19 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         }
         const int64_t groups = p.items_bound * kv_heads;
         if (groups > 2147483647) return fail(MVME_EINVAL, "paged prefill grid too large");
-        const bool scalar_pages = block_size % 4 == 0;
+        // Whole-tile pages need 32-bit per-lane offsets inside a tile.
+        const bool tile_pages = a.block_shift >= 6 && kv_heads * kPfD * 2 * kPfKeys < (int64_t(1) << 31);
+        const int pages = tile_pages ? kPagesPerTile : (block_size % 4 == 0 ? kPagesPerRows : kPagesPerLane);
         const dim3 grid((unsigned)groups), block(kPfThreads);
+        auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, s, a); };
         if (dtype == MVME_FP16) {
-            if (scalar_pages) hipLaunchKernelGGL((paged_prefill_mfma_kernel<Half, true>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((paged_prefill_mfma_kernel<Half, false>), grid, block, 0, s, a);
+            if (pages == kPagesPerTile) launch(paged_prefill_mfma_kernel<Half, kPagesPerTile>);
+            else if (pages == kPagesPerRows) launch(paged_prefill_mfma_kernel<Half, kPagesPerRows>);
+            else launch(paged_prefill_mfma_kernel<Half, kPagesPerLane>);
         } else {
-            if (scalar_pages) hipLaunchKernelGGL((paged_prefill_mfma_kernel<BFloat16, true>), grid, block, 0, s, a);
-            else hipLaunchKernelGGL((paged_prefill_mfma_kernel<BFloat16, false>), grid, block, 0, s, a);
+            if (pages == kPagesPerTile) launch(paged_prefill_mfma_kernel<BFloat16, kPagesPerTile>);
+            else if (pages == kPagesPerRows) launch(paged_prefill_mfma_kernel<BFloat16, kPagesPerRows>);
+            else launch(paged_prefill_mfma_kernel<BFloat16, kPagesPerLane>);
         }
         if (p.max_chunks > 1) {
             const dim3 grid((unsigned)total_tokens);
