@@ -73,6 +73,7 @@ struct PrefillArgs {
     const int64_t* lens;
     float* ws_o;   // [T, Hq, max_chunks, D] unnormalised partial outputs
     float* ws_ml;  // [T, Hq, max_chunks, 2] (running max in log2 units, sum)
+    int* ws_tok;   // [T] chunks of the token's query block (written by its chunk-0 items)
     int num_seqs;
     int q_heads;
     int kv_heads;
@@ -97,33 +98,46 @@ __device__ inline int64_t block_kv_end(const PrefillArgs& a, int64_t start, int6
     return e > 0 ? e : 0;
 }
 
+// kv_end <= table capacity < 2^31, so 32-bit unsigned arithmetic is exact.
 __device__ inline int chunks_of(const PrefillArgs& a, int64_t kv_end) {
-    return kv_end > 0 ? (int)((kv_end + a.chunk - 1) / a.chunk) : 1;
+    return kv_end > 0 ? (int)(((uint32_t)kv_end + (uint32_t)a.chunk - 1u) / (uint32_t)a.chunk) : 1;
 }
 
-// Items (query block x key chunk) of sequence s; every query block owns at
-// least one item so its rows always get written.
-__device__ inline int seq_items(const PrefillArgs& a, int s) {
-    const int64_t n = a.cu[s + 1] - a.cu[s];
+// Items (query block x key chunk) of a sequence with n packed queries;
+// every query block owns at least one item so its rows always get written.
+// Without key splitting every block is exactly one item.
+__device__ inline int seq_items(const PrefillArgs& a, int64_t n, int64_t start, int64_t ctx) {
     if (n <= 0) return 0;
-    const int64_t start = a.starts[s];
-    const int64_t ctx = a.lens[s];
+    if (a.max_chunks == 1) return (int)((n + a.qb - 1) / a.qb);
     int count = 0;
     for (int64_t b0 = 0; b0 < n; b0 += a.qb) count += chunks_of(a, block_kv_end(a, start, ctx, n, b0));
     return count;
 }
 
-// Item `item` -> (sequence, first query token, chunk, kv_end, chunks).
-// Lane-parallel: each lane counts the items of one sequence, a wave prefix
-// sum locates the sequence, then the query blocks of that one sequence are
-// walked.  Every wave of the work-group computes the same answer.
-__device__ inline bool find_item(const PrefillArgs& a, int item, int& seq, int& q0, int& chunk,
-                                 int64_t& kv_end, int& nchunks) {
+struct PrefillItem {
+    int seq, q0, chunk, nchunks;
+    int64_t kv_end;
+    int64_t row0, qlen, start, ctx;  // the sequence's metadata
+};
+
+// Item `item` -> sequence, first query token, chunk, and the sequence's
+// metadata.  Lane-parallel: each lane loads one sequence's metadata and
+// counts its items, a wave prefix sum locates the sequence, the lane that
+// owns it hands its metadata over by shuffles, and that one sequence's query
+// blocks are walked.  Every wave of the work-group computes the same answer.
+__device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it) {
     const int lane = __lane_id();
     int base = 0;
     for (int s0 = 0; s0 < a.num_seqs; s0 += kWave) {
         const int s = s0 + lane;
-        const int cnt = s < a.num_seqs ? seq_items(a, s) : 0;
+        int64_t row0 = 0, n = 0, start = 0, ctx = 0;
+        if (s < a.num_seqs) {
+            row0 = a.cu[s];
+            n = a.cu[s + 1] - row0;
+            start = a.starts[s];
+            ctx = a.lens[s];
+        }
+        const int cnt = seq_items(a, n, start, ctx);
         int incl = cnt;
 #pragma unroll
         for (int off = 1; off < kWave; off <<= 1) {
@@ -134,19 +148,20 @@ __device__ inline bool find_item(const PrefillArgs& a, int item, int& seq, int& 
         if (item < base + total) {
             const uint64_t hit = __ballot(base + incl > item);
             const int sel = __builtin_ctzll(hit);
-            seq = s0 + sel;
+            it.seq = s0 + sel;
             int rem = item - base - (__shfl(incl, sel) - __shfl(cnt, sel));
-            const int64_t n = a.cu[seq + 1] - a.cu[seq];
-            const int64_t start = a.starts[seq];
-            const int64_t ctx = a.lens[seq];
-            for (int64_t b0 = 0; b0 < n; b0 += a.qb) {
-                const int64_t e = block_kv_end(a, start, ctx, n, b0);
+            it.row0 = __shfl(row0, sel);
+            it.qlen = __shfl(n, sel);
+            it.start = __shfl(start, sel);
+            it.ctx = __shfl(ctx, sel);
+            for (int64_t b0 = 0; b0 < it.qlen; b0 += a.qb) {
+                const int64_t e = block_kv_end(a, it.start, it.ctx, it.qlen, b0);
                 const int nc = chunks_of(a, e);
                 if (rem < nc) {
-                    q0 = (int)b0;
-                    chunk = rem;
-                    kv_end = e;
-                    nchunks = nc;
+                    it.q0 = (int)b0;
+                    it.chunk = rem;
+                    it.kv_end = e;
+                    it.nchunks = nc;
                     return true;
                 }
                 rem -= nc;
@@ -250,27 +265,30 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
     __shared__ __attribute__((aligned(16))) float sm_b[kPfStages][kPfKeys];
     __shared__ __attribute__((aligned(16))) int sm_full[kPfStages][kPfWaves];
 
-    int seq, q0, chunk, nchunks;
-    int64_t kv_end64;
-    if (!find_item(a, blockIdx.x / a.kv_heads, seq, q0, chunk, kv_end64, nchunks)) return;
+    PrefillItem item;
+    if (!find_item(a, blockIdx.x / a.kv_heads, item)) return;
     // The item is the same for every lane: keep it in scalar registers.
-    seq = __builtin_amdgcn_readfirstlane(seq);
-    q0 = __builtin_amdgcn_readfirstlane(q0);
-    chunk = __builtin_amdgcn_readfirstlane(chunk);
-    nchunks = __builtin_amdgcn_readfirstlane(nchunks);
-    kv_end64 = __builtin_amdgcn_readfirstlane((int)kv_end64);
+    // Context positions fit in 31 bits (table capacity <= 2^31 keys), and so
+    // do the packed row index and query count (T*Hq < 2^31).
+    const int seq = __builtin_amdgcn_readfirstlane(item.seq);
+    const int q0 = __builtin_amdgcn_readfirstlane(item.q0);
+    const int chunk = __builtin_amdgcn_readfirstlane(item.chunk);
+    const int nchunks = __builtin_amdgcn_readfirstlane(item.nchunks);
+    const int64_t kv_end64 = __builtin_amdgcn_readfirstlane((int)item.kv_end);
+    const int64_t row0 = __builtin_amdgcn_readfirstlane((int)item.row0);
+    const int qlen = __builtin_amdgcn_readfirstlane((int)item.qlen);
+    const int64_t ctx = item.ctx;
     const int kvh = blockIdx.x % a.kv_heads;
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     const int li = lane & 15;  // MFMA row / column index
     const int lg = lane >> 4;  // MFMA k-group (0..3)
 
-    // Context positions fit in 31 bits (table capacity <= 2^31 keys).
-    const int64_t row0 = a.cu[seq];
-    const int qlen = (int)(a.cu[seq + 1] - row0);
-    const int start = (int)a.starts[seq];
-    const int64_t ctx = a.lens[seq];
     const int cap = a.table_width * a.block_size;
+    // A row is valid only at positions in [0, cap); clamping start to
+    // [-1, cap] keeps every row's validity and its position in 32 bits.
+    const int start = __builtin_amdgcn_readfirstlane(
+        (int)(item.start < -1 ? -1 : (item.start > cap ? (int64_t)cap : item.start)));
     const int64_t* table = a.tables + (int64_t)seq * a.table_width;
     const int kv_end = (int)kv_end64;
     const int chunk_start = chunk * a.chunk;
@@ -287,8 +305,9 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
         const int r = wave * (16 * kPfNb) + nb * 16 + li;
         qi[nb] = q0 + r % a.qb;
         head[nb] = kvh * a.group + r / a.qb;
-        pos[nb] = start + qi[nb];
-        row_ok[nb] = qi[nb] < qlen && start >= 0 && pos[nb] < ctx && pos[nb] < cap;
+        const int64_t p64 = (int64_t)start + qi[nb];
+        row_ok[nb] = qi[nb] < qlen && start >= 0 && p64 < ctx && p64 < cap;
+        pos[nb] = (int)p64;
         if (row_ok[nb]) {
             wave_last = max(wave_last, pos[nb]);
             wave_first = min(wave_first, pos[nb]);
@@ -304,19 +323,6 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
     wave_last = __builtin_amdgcn_readfirstlane(wave_last);
     wave_first = __builtin_amdgcn_readfirstlane(wave_first);
 
-    // Q^T operands: row (nb, li), d = 32*dc + 8*lg .. +8.  Loaded (and waited
-    // for) before any tile copy is issued, so the copies own the counter.
-    u32x4 qop[kPfNb][4];
-#pragma unroll
-    for (int nb = 0; nb < kPfNb; ++nb) {
-        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + ((row0 + qi[nb]) * a.q_heads + head[nb]) * kPfD;
-#pragma unroll
-        for (int dc = 0; dc < 4; ++dc) {
-            qop[nb][dc] = u32x4{0u, 0u, 0u, 0u};
-            if (row_ok[nb]) qop[nb][dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
-        }
-    }
-    wait_vmcnt_all();
 
     float m_run[kPfNb], l_part[kPfNb];
     f32x4 o[kPfNb][8];
@@ -429,16 +435,50 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
         if (lane == 0) sm_full[st][wave] = wave_full ? 1 : 0;
     };
 
+    // Page ids of the first tiles (scalar loads) go out before the Q loads
+    // so that both latencies overlap.
+    int pro_pg[kPfAhead + 1];
+    if constexpr (PAGES == kPagesPerTile) {
+#pragma unroll
+        for (int k = 0; k <= kPfAhead; ++k) {
+            lookup(t_begin + k);
+            pro_pg[k] = pg_next[0];
+        }
+    }
+    // Q^T operands: row (nb, li), d = 32*dc + 8*lg .. +8.  Loaded (and waited
+    // for) before any tile copy is issued, so the copies own the counter.
+    u32x4 qop[kPfNb][4];
+#pragma unroll
+    for (int nb = 0; nb < kPfNb; ++nb) {
+        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + ((row0 + qi[nb]) * a.q_heads + head[nb]) * kPfD;
+#pragma unroll
+        for (int dc = 0; dc < 4; ++dc) {
+            qop[nb][dc] = u32x4{0u, 0u, 0u, 0u};
+            if (row_ok[nb]) qop[nb][dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
+        }
+    }
+    wait_vmcnt_all();
+
     // Prologue: tiles t_begin .. t_begin+kPfAhead-1 in flight (copies of
     // tiles past the chunk read zeros into stages nobody computes on, which
     // keeps the per-iteration copy count constant).
     if (t_begin < t_end) {
 #pragma unroll
         for (int k = 0; k < kPfAhead; ++k) {
-            lookup(t_begin + k);
+            if constexpr (PAGES == kPagesPerTile) {
+#pragma unroll
+                for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pro_pg[k];
+            } else {
+                lookup(t_begin + k);
+            }
             issue(t_begin + k, k);
         }
-        lookup(t_begin + kPfAhead);
+        if constexpr (PAGES == kPagesPerTile) {
+#pragma unroll
+            for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pro_pg[kPfAhead];
+        } else {
+            lookup(t_begin + kPfAhead);
+        }
     }
     int st = kPfStages - 1;  // ring position of `tile` (advanced at the top of the loop)
     for (int tile = t_begin; tile < t_end; ++tile) {
@@ -607,48 +647,67 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
             }
         }
     }
+    // With key splitting, the first chunk's item of kv head 0 tells the merge
+    // how many chunks each of its block's tokens has (1: written directly).
+    if (a.max_chunks > 1 && chunk == 0 && kvh == 0) {
+        for (int t = threadIdx.x; t < a.qb && q0 + t < qlen; t += kPfThreads) a.ws_tok[row0 + q0 + t] = nchunks;
+    }
 }
 
 // Combines the key-chunk partials of rows whose query block needed several
 // chunks: out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
-// One work-group per packed token (the sequence lookup happens once for all
-// heads); thread t handles head t/16, dims 8*(t%16) .. +8.
+// One work-group per packed token (its chunk count comes from the attention
+// kernel); thread t handles head t/16, dims 8*(t%16) .. +8.
 constexpr int kMergeThreads = 256;
 
 template <typename T>
 __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(PrefillArgs a) {
     const int64_t token = blockIdx.x;
-    int lo = 0, hi = a.num_seqs;
-    while (lo < hi) {
-        const int mid = (lo + hi) / 2;
-        if (a.cu[mid + 1] <= token) lo = mid + 1;
-        else hi = mid;
-    }
-    if (lo >= a.num_seqs || token < a.cu[lo]) return;
-    const int64_t n = a.cu[lo + 1] - a.cu[lo];
-    const int64_t qi = token - a.cu[lo];
-    const int64_t b0 = qi / a.qb * a.qb;
-    const int nchunks = chunks_of(a, block_kv_end(a, a.starts[lo], a.lens[lo], n, b0));
+    // Every token of consistent metadata is written by its block's first
+    // item; the clamp keeps reads inside the workspace for any other value.
+    const int nchunks = min(a.ws_tok[token], a.max_chunks);
     if (nchunks <= 1) return;
+    constexpr int kGroup = 4;  // chunks whose partials are loaded together
     for (int idx = threadIdx.x; idx < a.q_heads * (kPfD / 8); idx += kMergeThreads) {
         const int head = idx / (kPfD / 8);
         const int d0 = 8 * (idx % (kPfD / 8));
         const int64_t slot0 = (token * a.q_heads + head) * a.max_chunks;
         const float* ml = a.ws_ml + slot0 * 2;
         float mx = kNegInf;
-        for (int c = 0; c < nchunks; ++c) mx = fmaxf(mx, ml[2 * c]);
+        for (int c0 = 0; c0 < nchunks; c0 += kGroup) {
+#pragma unroll
+            for (int k = 0; k < kGroup; ++k)
+                if (c0 + k < nchunks) mx = fmaxf(mx, ml[2 * (c0 + k)]);
+        }
         const float ref = mx == kNegInf ? 0.f : mx;
         float sum = 0.f;
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int c = 0; c < nchunks; ++c) {
-            const float w = fast_exp2(ml[2 * c] - ref);
-            sum += ml[2 * c + 1] * w;
-            const f32x4* po = reinterpret_cast<const f32x4*>(a.ws_o + (slot0 + c) * kPfD + d0);
-            const f32x4 x0 = po[0], x1 = po[1];
+        for (int c0 = 0; c0 < nchunks; c0 += kGroup) {
+            // All loads of the group first, so that they are in flight together.
+            f32x4 x[kGroup][2];
+            float mc[kGroup], lc[kGroup];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                acc[i] = fmaf(x0[i], w, acc[i]);
-                acc[4 + i] = fmaf(x1[i], w, acc[4 + i]);
+            for (int k = 0; k < kGroup; ++k) {
+                x[k][0] = x[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                mc[k] = kNegInf;
+                lc[k] = 0.f;
+                if (c0 + k < nchunks) {
+                    const f32x4* po = reinterpret_cast<const f32x4*>(a.ws_o + (slot0 + c0 + k) * kPfD + d0);
+                    x[k][0] = po[0];
+                    x[k][1] = po[1];
+                    mc[k] = ml[2 * (c0 + k)];
+                    lc[k] = ml[2 * (c0 + k) + 1];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kGroup; ++k) {
+                const float w = mc[k] == kNegInf ? 0.f : fast_exp2(mc[k] - ref);
+                sum = fmaf(lc[k], w, sum);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    acc[i] = fmaf(x[k][0][i], w, acc[i]);
+                    acc[4 + i] = fmaf(x[k][1][i], w, acc[4 + i]);
+                }
             }
         }
         const float inv = sum > 0.f ? 1.f / sum : 0.f;
@@ -829,7 +888,9 @@ extern "C" size_t mvme_paged_prefill_workspace_size(int64_t num_seqs, int64_t to
     const PrefillPlan p = make_prefill_plan(num_seqs, total_tokens, q_heads, kv_heads, head_dim, block_size,
                                             table_width, chunk_tokens);
     if (!p.mfma || p.max_chunks <= 1) return 0;
-    return (size_t)total_tokens * q_heads * p.max_chunks * (kPfD + 2) * sizeof(float);
+    // Partials (O, then max/sum), then one int per token, 16-byte aligned.
+    const size_t partials = (size_t)total_tokens * q_heads * p.max_chunks * (kPfD + 2) * sizeof(float);
+    return partials + ((size_t)total_tokens * sizeof(int) + 15) / 16 * 16;
 }
 
 extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void* key_cache,
@@ -884,6 +945,7 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         if (need > 0) {
             a.ws_o = static_cast<float*>(workspace);
             a.ws_ml = a.ws_o + total_tokens * q_heads * p.max_chunks * kPfD;
+            a.ws_tok = reinterpret_cast<int*>(a.ws_ml + total_tokens * q_heads * p.max_chunks * 2);
         }
         const int64_t groups = p.items_bound * kv_heads;
         if (groups > 2147483647) return fail(MVME_EINVAL, "paged prefill grid too large");

@@ -87,7 +87,7 @@ def test_scatter_and_prefill_reject_bad_arguments(lib):
     assert "1024" in lib.last_error()
     # Few query blocks + long table: key-chunk split needs a workspace.
     need = lib.prefill_workspace_size(8, 1024, 16, 8, 128, 256, 16, 0)
-    assert need == 1024 * 16 * 8 * (128 + 2) * 4
+    assert need == 1024 * 16 * 8 * (128 + 2) * 4 + 1024 * 4
     assert _status(lib, "mvme_paged_prefill_attention", 1, 1, 1, 1, 1, 1, 1, 1, 8, 1024, 16, 8, 128, 200, 256, 16,
                    0, 0, None, 0, None) == ext.EWORKSPACE
     # Many query blocks: no split, no workspace.
