@@ -74,6 +74,7 @@ struct PrefillArgs {
     float* ws_o;   // [T, Hq, max_chunks, D] unnormalised partial outputs
     float* ws_ml;  // [T, Hq, max_chunks, 2] (running max in log2 units, sum)
     int* ws_tok;   // [T] chunks of the token's query block (written by its chunk-0 items)
+    int item_stride;  // 0: one item per work-group; else items walked per work-group
     int num_seqs;
     int q_heads;
     int kv_heads;
@@ -257,16 +258,22 @@ constexpr int kPagesPerTile = 2;
 // copies, and "tile t has landed" is exactly vmcnt <= 2 tiles of copies.
 // Otherwise page ids are per-lane vector loads and every tile waits for
 // all outstanding copies (correct, shallower pipeline).
-template <typename T, int PAGES>
-__global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(PrefillArgs a) {
-    constexpr bool SCALAR_PAGES = PAGES != kPagesPerLane;
-    __shared__ __attribute__((aligned(16))) uint8_t sm_k[kPfStages][kTileBytes];
-    __shared__ __attribute__((aligned(16))) uint8_t sm_v[kPfStages][kTileBytes];
-    __shared__ __attribute__((aligned(16))) float sm_b[kPfStages][kPfKeys];
-    __shared__ __attribute__((aligned(16))) int sm_full[kPfStages][kPfWaves];
+struct PrefillLds {
+    alignas(16) uint8_t k[kPfStages][kTileBytes];
+    alignas(16) uint8_t v[kPfStages][kTileBytes];
+    alignas(16) float b[kPfStages][kPfKeys];
+    alignas(16) int full[kPfStages][kPfWaves];
+};
 
-    PrefillItem item;
-    if (!find_item(a, blockIdx.x / a.kv_heads, item)) return;
+// One work item, computed by the whole work-group.
+template <typename T, int PAGES>
+__device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a, const PrefillItem& item,
+                                                            PrefillLds& lds) {
+    constexpr bool SCALAR_PAGES = PAGES != kPagesPerLane;
+    auto& sm_k = lds.k;
+    auto& sm_v = lds.v;
+    auto& sm_b = lds.b;
+    auto& sm_full = lds.full;
     // The item is the same for every lane: keep it in scalar registers.
     // Context positions fit in 31 bits (table capacity <= 2^31 keys), and so
     // do the packed row index and query count (T*Hq < 2^31).
@@ -654,6 +661,28 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
     }
 }
 
+// Items are enumerated densely, so the first index past the end ends a
+// work-group's walk.  WALK = false: one item per work-group (the grid covers
+// every possible item).  WALK = true: one work-group per CU slot, each
+// walking items idx, idx + item_stride, ... (a separate instantiation, so
+// that the one-item kernel keeps its register allocation).
+template <typename T, int PAGES, bool WALK>
+__global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) PrefillLds lds;
+    if constexpr (!WALK) {
+        PrefillItem item;
+        if (!find_item(a, blockIdx.x / a.kv_heads, item)) return;
+        prefill_item<T, PAGES>(a, item, lds);
+    } else {
+        for (int idx = blockIdx.x / a.kv_heads;; idx += a.item_stride) {
+            PrefillItem item;
+            if (!find_item(a, idx, item)) return;
+            prefill_item<T, PAGES>(a, item, lds);
+            __syncthreads();  // every wave is done with the LDS ring before the next item refills it
+        }
+    }
+}
+
 // Combines the key-chunk partials of rows whose query block needed several
 // chunks: out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
 // One work-group per packed token (its chunk count comes from the attention
@@ -947,21 +976,51 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
             a.ws_ml = a.ws_o + total_tokens * q_heads * p.max_chunks * kPfD;
             a.ws_tok = reinterpret_cast<int*>(a.ws_ml + total_tokens * q_heads * p.max_chunks * 2);
         }
-        const int64_t groups = p.items_bound * kv_heads;
+        // The item count depends on lengths that stay on the device, so the
+        // grid is sized from a bound.  With key splitting that bound is loose
+        // (every block counted with the most chunks) and surplus work-groups
+        // would queue behind the real ones (one work-group fits a CU): there
+        // the grid is one work-group per CU slot, each walking its items.
+        int64_t item_slots = p.items_bound;
+        a.item_stride = 0;
+        if (p.max_chunks > 1) {
+            const int64_t slots = std::max<int64_t>(1, kPrefillCUs / kv_heads);
+            if (p.items_bound > slots) {
+                item_slots = slots;
+                a.item_stride = (int)slots;
+            }
+        }
+        const int64_t groups = item_slots * kv_heads;
         if (groups > 2147483647) return fail(MVME_EINVAL, "paged prefill grid too large");
         // Whole-tile pages need 32-bit per-lane offsets inside a tile.
         const bool tile_pages = a.block_shift >= 6 && kv_heads * kPfD * 2 * kPfKeys < (int64_t(1) << 31);
         const int pages = tile_pages ? kPagesPerTile : (block_size % 4 == 0 ? kPagesPerRows : kPagesPerLane);
         const dim3 grid((unsigned)groups), block(kPfThreads);
         auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, s, a); };
+        auto launch_walk = [&](auto one, auto walk) {
+            if (a.item_stride > 0) launch(walk);
+            else launch(one);
+        };
         if (dtype == MVME_FP16) {
-            if (pages == kPagesPerTile) launch(paged_prefill_mfma_kernel<Half, kPagesPerTile>);
-            else if (pages == kPagesPerRows) launch(paged_prefill_mfma_kernel<Half, kPagesPerRows>);
-            else launch(paged_prefill_mfma_kernel<Half, kPagesPerLane>);
+            if (pages == kPagesPerTile)
+                launch_walk(paged_prefill_mfma_kernel<Half, kPagesPerTile, false>,
+                            paged_prefill_mfma_kernel<Half, kPagesPerTile, true>);
+            else if (pages == kPagesPerRows)
+                launch_walk(paged_prefill_mfma_kernel<Half, kPagesPerRows, false>,
+                            paged_prefill_mfma_kernel<Half, kPagesPerRows, true>);
+            else
+                launch_walk(paged_prefill_mfma_kernel<Half, kPagesPerLane, false>,
+                            paged_prefill_mfma_kernel<Half, kPagesPerLane, true>);
         } else {
-            if (pages == kPagesPerTile) launch(paged_prefill_mfma_kernel<BFloat16, kPagesPerTile>);
-            else if (pages == kPagesPerRows) launch(paged_prefill_mfma_kernel<BFloat16, kPagesPerRows>);
-            else launch(paged_prefill_mfma_kernel<BFloat16, kPagesPerLane>);
+            if (pages == kPagesPerTile)
+                launch_walk(paged_prefill_mfma_kernel<BFloat16, kPagesPerTile, false>,
+                            paged_prefill_mfma_kernel<BFloat16, kPagesPerTile, true>);
+            else if (pages == kPagesPerRows)
+                launch_walk(paged_prefill_mfma_kernel<BFloat16, kPagesPerRows, false>,
+                            paged_prefill_mfma_kernel<BFloat16, kPagesPerRows, true>);
+            else
+                launch_walk(paged_prefill_mfma_kernel<BFloat16, kPagesPerLane, false>,
+                            paged_prefill_mfma_kernel<BFloat16, kPagesPerLane, true>);
         }
         if (p.max_chunks > 1) {
             const dim3 grid((unsigned)total_tokens);

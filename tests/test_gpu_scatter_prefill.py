@@ -209,3 +209,22 @@ def test_c5_chunked_prefill_full_size():
     # Scatter bit-exactness at full size: every new row sits in its slot.
     rows = case["key_cache"].view(-1, 8, 128)[case["slot_mapping"]]
     assert torch.equal(rows, case["new_key"])
+
+
+@pytest.mark.parametrize("dtype,block_size,chunk_tokens", [
+    (torch.bfloat16, 256, 0), (torch.float16, 16, 0), (torch.bfloat16, 256, 192),
+])
+def test_prefill_work_groups_walk_several_items(dtype, block_size, chunk_tokens):
+    """Few query blocks over long contexts: the keys are split into more chunk
+    items than there are CU slots, so each work-group walks several items and
+    the merge combines up to 37 partials per row."""
+    priors = [7000, 3000, 5000, 6100] * 4
+    case = workloads.chunked_prefill_case(device=DEV, num_seqs=16, new_tokens=64, block_size=block_size,
+                                          dtype=dtype, priors=priors, seed=11)
+    write_kv_cache_slots(case["key_cache"], case["value_cache"], case["slot_mapping"], case["new_key"],
+                         case["new_value"], backend="hip")
+    names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+    args = [case[n] for n in names]
+    actual = paged_prefill_attention(*args, block_size, backend="hip", chunk_tokens=chunk_tokens)
+    expected = paged_oracle.paged_prefill_attention(*[a.cpu() for a in args], block_size, cast=False)
+    assert max_err(actual, expected) <= GATE[dtype]
