@@ -127,6 +127,42 @@ def headline_parity(layers, oracle):
     return {"layers_checked": [0, LAYERS - 1], "max_abs_error": worst, "gate": 2e-3, "passed": worst <= 2e-3}
 
 
+def decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_attention, oracle):
+    """The decode step as the engine runs it per layer (native_qwen3.py:179-197):
+    write the batch's new K/V row at position len-1 of every sequence
+    (write_kv_cache_batch), then paged attention over the updated context --
+    28 layers in one captured graph (the "--cuda-graph" decode step with the
+    hip backend).  Reuses the headline layers; changes their last KV row."""
+    gen = torch.Generator(device="cuda").manual_seed(BASE_SEED + 77)
+    for c in layers:
+        c["new_key"] = torch.randn((BATCH, HKV, D), generator=gen, device="cuda").half()
+        c["new_value"] = torch.randn((BATCH, HKV, D), generator=gen, device="cuda").half()
+        c["offsets"] = (c["context_lens"] - 1).contiguous()
+
+    def step():
+        for c in layers:
+            write_kv_cache_batch(c["key_cache"], c["value_cache"], c["block_tables"], c["offsets"], c["new_key"],
+                                 c["new_value"], BLOCK, backend="hip", validate=False)
+            paged_attention(c["query"], c["key_cache"], c["value_cache"], c["block_tables"], c["context_lens"],
+                            BLOCK, backend="hip", validate=False, out=c["out"])
+
+    ms, _ = graph_time_ms(step, torch, calls_per_graph=2 * LAYERS, replays=args.steps, warmup=args.warmup)
+    c = layers[0]
+    tables, offsets = c["block_tables"].cpu(), c["offsets"].cpu()
+    pages = tables[torch.arange(BATCH), offsets // BLOCK]
+    rows_k = c["key_cache"].cpu()[pages, offsets % BLOCK]
+    rows_v = c["value_cache"].cpu()[pages, offsets % BLOCK]
+    scatter_ok = torch.equal(rows_k, c["new_key"].cpu()) and torch.equal(rows_v, c["new_value"].cpu())
+    tensors = {"query": c["query"].cpu(), "key_cache": c["key_cache"].cpu(), "value_cache": c["value_cache"].cpu(),
+               "block_tables": tables, "context_lens": c["context_lens"].cpu()}
+    err = max_abs(c["out"], oracle.fp32_oracle(tensors, BLOCK))
+    step_bytes = LAYERS * (layer_bytes() + 2 * BATCH * HKV * D * 2 * 2 + BATCH * 8)
+    return {"us_per_step": ms * 1e3, "us_per_layer": ms * 1e3 / LAYERS,
+            "TBps": step_bytes / (ms * 1e-3) / 1e12, "launches_per_step": 2 * LAYERS,
+            "scatter_bit_exact": scatter_ok, "max_abs_error_layer0": err, "gate": 2e-3,
+            "passed": scatter_ok and err <= 2e-3}
+
+
 def cpu_baseline(layers, oracle, torch, budget_s):
     """The reference's torch decode path, restated in the oracle, on host cores."""
     threads = torch.get_num_threads()
@@ -304,7 +340,7 @@ def main(argv=None):
     import torch
 
     from mini_engine_hip.kernels import hip_extension
-    from mini_engine_hip.kernels.data import write_kv_cache_slots
+    from mini_engine_hip.kernels.data import write_kv_cache_batch, write_kv_cache_slots
     from mini_engine_hip.kernels.paged import paged_attention
     from mini_engine_hip.kernels.prefill import paged_prefill_attention
     from mini_engine_hip import workloads
@@ -336,6 +372,11 @@ def main(argv=None):
     log(f"headline: {step_ms:.3f} ms/step, {per_call_ms * 1e3:.2f} us/call, {achieved_gbs:.0f} GB/s")
     parity = headline_parity(layers, paged_oracle)
     log(f"parity: {parity}")
+    decode_step = None
+    if not args.no_extra:
+        decode_step = decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_attention,
+                                               paged_oracle)
+        log(f"decode step with scatter: {decode_step}")
 
     traffic = None
     traffic_file = ROOT / "profiles" / "paged_decode_b32_ctx2048_traffic.txt"
@@ -375,6 +416,7 @@ def main(argv=None):
     if not args.no_extra:
         result["extra"] = extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention,
                                           workloads, paged_oracle, names=tuple(args.extra.split(",")))
+        result["extra"]["decode_step_b32_ctx2048_28layers_with_scatter"] = decode_step
         log(f"extra: {json.dumps(result['extra'])}")
     if not args.no_cpu_baseline:
         gen_layers = [workloads.decode_b32_layer(torch.device("cuda:0"), seed=BASE_SEED + 2)]
