@@ -199,7 +199,7 @@ def cpu_baseline(layers, oracle, torch, budget_s):
 # Other workloads of the path (reported under "extra").
 # ---------------------------------------------------------------------------
 
-EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill")
+EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "norm_rope")
 
 
 def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, oracle,
@@ -214,6 +214,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         _extra_ragged(torch, paged_attention, workloads, oracle, dev, extra)
     if "prefill" in names:
         _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, oracle, dev, extra)
+    if "norm_rope" in names:
+        _extra_norm_rope(torch, oracle, dev, extra)
     return extra
 
 
@@ -314,6 +316,95 @@ def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloa
         "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "GBps": kv_bytes / per_call / 1e9, "flops": flops, "priors": c["priors"],
         "max_abs_error": max_abs(holder["out"], ref)}
+
+
+def _norm_rope_case(torch, dev, tokens, dtype, seed):
+    gen = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn(tokens, (HQ + 2 * HKV) * D, generator=gen) * 3).to(dtype)
+    angles = torch.randn(tokens, D // 2, generator=gen) * 4
+    c = {"qkv": qkv, "cos": angles.cos().to(dtype), "sin": angles.sin().to(dtype),
+         "wq": (torch.rand(D, generator=gen) + 0.5).to(dtype), "wk": (torch.rand(D, generator=gen) + 0.5).to(dtype)}
+    c = {k: v.to(dev) for k, v in c.items()}
+    c["q"] = c["qkv"][:, :HQ * D].view(tokens, HQ, D)
+    c["k"] = c["qkv"][:, HQ * D:(HQ + HKV) * D].view(tokens, HKV, D)
+    c["v"] = c["qkv"][:, (HQ + HKV) * D:].view(tokens, HKV, D)
+    return c
+
+
+def _extra_norm_rope(torch, oracle, dev, extra):
+    """Fused q/k RMSNorm + RoPE + KV write at the prefill batch (1024 tokens, bf16, block 256, slot
+    mapping) and the decode batch (32 sequences, fp16, block 256, tables + positions), beside the same
+    four steps as separate eager torch ops plus the HIP scatter (the reference's torch data path, timed
+    eagerly on the stream, not captured)."""
+    from mini_engine_hip.kernels.rope import qk_norm_rope_write_kv
+    from mini_engine_hip.kernels.data import write_kv_cache_slots
+
+    for name, tokens, dtype, mode in (("norm_rope_kv_write_prefill_1024tok_bf16", 1024, torch.bfloat16, "slots"),
+                                      ("norm_rope_kv_write_decode_b32_fp16", 32, torch.float16, "tables")):
+        c = _norm_rope_case(torch, dev, tokens, dtype, seed=BASE_SEED + tokens)
+        pages = 300                   # distinct pages for every decode sequence (32 x 8 table entries)
+        gen = torch.Generator().manual_seed(BASE_SEED + 7)
+        kc = torch.randn(pages, BLOCK, HKV, D, generator=gen).to(dtype).to(dev)
+        vc = torch.randn(pages, BLOCK, HKV, D, generator=gen).to(dtype).to(dev)
+        slots = torch.randperm(pages * BLOCK, generator=gen)[:tokens].to(dev)
+        meta = {"slot_mapping": slots}
+        if mode == "tables":
+            width = 8
+            tables = torch.randperm(pages, generator=gen)[:tokens * width].view(tokens, width).to(dev)
+            positions = torch.randint(0, width * BLOCK, (tokens,), generator=gen).to(dev)
+            meta = {"block_tables": tables, "positions": positions}
+            flat = (tables.gather(1, (positions // BLOCK)[:, None])[:, 0] * BLOCK + positions % BLOCK)
+            slots = flat
+        out = torch.empty(tokens, HQ, D, dtype=dtype, device=dev)
+        args = (c["q"], c["k"], c["v"], c["wq"], c["wk"], c["cos"], c["sin"], kc, vc)
+        fused = lambda: qk_norm_rope_write_kv(*args, validate=False, out=out, **meta)  # noqa: E731
+
+        def eager_four_steps():
+            q = c["q"].float()
+            q = (q * torch.rsqrt(q.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype) * c["wq"]
+            k = c["k"].float()
+            k = (k * torch.rsqrt(k.pow(2).mean(-1, keepdim=True) + 1e-6)).to(dtype) * c["wk"]
+            cs, sn, half = c["cos"].unsqueeze(1), c["sin"].unsqueeze(1), D // 2
+            q = torch.cat((q[..., :half] * cs - q[..., half:] * sn, q[..., :half] * sn + q[..., half:] * cs), -1)
+            k = torch.cat((k[..., :half] * cs - k[..., half:] * sn, k[..., :half] * sn + k[..., half:] * cs), -1)
+            write_kv_cache_slots(kc, vc, slots, k, c["v"], backend="hip", validate=False)
+            return q
+
+        def many(fn, n):
+            def run():
+                for _ in range(n):
+                    fn()
+            return run
+        ms, _ = graph_time_ms(many(fused, 50), torch, calls_per_graph=50, replays=20, warmup=3)
+        eager_four_steps()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        many(eager_four_steps, 10)()
+        end.record()
+        end.synchronize()
+        eager_ms = start.elapsed_time(end)
+        per_call = ms / 50 * 1e-3
+        moved = (tokens * (HQ + 2 * HKV) * D * 2 + tokens * D * 2 + 2 * D * 2 + tokens * 8 * (2 if mode == "tables"
+                 else 1) + tokens * HQ * D * 2 + tokens * 2 * HKV * D * 2)
+        # Parity of the last call against the oracle (q rows; written K rows; V rows bit-exact).
+        fused()
+        torch.cuda.synchronize()
+        cpu = {k: v.cpu() for k, v in c.items()}
+        kc_o, vc_o = torch.zeros(pages, BLOCK, HKV, D, dtype=dtype), torch.zeros(pages, BLOCK, HKV, D, dtype=dtype)
+        cpu_meta = {k: v.cpu() for k, v in meta.items()}
+        want_q = oracle.qk_norm_rope_write_kv(cpu["q"], cpu["k"], cpu["v"], cpu["wq"], cpu["wk"], cpu["cos"],
+                                              cpu["sin"], kc_o, vc_o, **cpu_meta)
+        rows = slots.cpu()
+        got_k, want_k = kc.cpu().view(-1, HKV, D)[rows], kc_o.view(-1, HKV, D)[rows]
+        extra[name] = {
+            "us_per_call": per_call * 1e6, "GBps": moved / per_call / 1e9,
+            "frac_of_hbm_peak": moved / per_call / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": moved,
+            "eager_torch_four_steps_us": eager_ms / 10 * 1e3,
+            "q_max_abs_error": max_abs(out, want_q),
+            "q_bit_identical_frac": (out.cpu() == want_q).float().mean().item(),
+            "k_max_abs_error": max_abs(got_k, want_k),
+            "v_bit_exact": bool(torch.equal(vc.cpu().view(-1, HKV, D)[rows], vc_o.view(-1, HKV, D)[rows]))}
 
 
 def main(argv=None):

@@ -180,6 +180,44 @@ int mvme_paged_prefill_attention(void* out, const void* q,
                                  int64_t chunk_tokens, int dtype,
                                  void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * Fused per-head q/k RMSNorm + rotary embedding + KV page write (the step
+ * before paged attention).  For every token t:
+ *   q_out[t, h]             = rope(rmsnorm(q[t, h], q_weight))  (h < q_heads)
+ *   key_cache[slot(t), h]   = rope(rmsnorm(k[t, h], k_weight))  (h < kv_heads)
+ *   value_cache[slot(t), h] = v[t, h]                           (bit-exact)
+ * rmsnorm(x, w) = T(T(x / sqrt(mean(x^2) + eps)) * w); rope rotates the halves
+ * [0, D/2) and [D/2, D) with cos[t, :], sin[t, :] ([tokens, head_dim/2]),
+ * rounding each product to fp16/bf16 before the add/subtract (the eager
+ * rounding the reference matches).  slot(t) = slot_mapping[t] when
+ * slot_mapping is non-null (prefill), else page*block_size + pos%block_size
+ * with pos = positions[t] and page = block_tables[t, pos/block_size]
+ * (decode, one token per sequence).  Tokens with an invalid slot still get
+ * q_out and skip the cache write.  q/k/v rows are `*_token_stride` elements
+ * apart (slices of a fused QKV projection); their [heads, head_dim] part is
+ * dense.  head_dim even and <= 512.
+ * Replaces the sequence q_norm / k_norm (RMSNorm, mini_engine/kernels/
+ *   elementwise.py:16-21 -> csrc/elementwise.cu norm_kernel, bindings.cpp:63-66),
+ *   apply_rope (kernels/data.py:27-36 -> csrc/data.cu:29-65, bindings.cpp:96-108)
+ *   and write_kv_cache_slots / write_kv_cache_batch (data.py:84-130, :67-81)
+ *   that Attention._forward_prefill_batch and forward_decode_batch run
+ *   (mini_engine/model/native_qwen3.py:150-157, :179-191): one launch instead
+ *   of four.
+ */
+int mvme_qk_norm_rope_write_kv(void* q_out, void* key_cache, void* value_cache,
+                               int64_t num_blocks, int64_t block_size,
+                               int64_t kv_heads, int64_t head_dim,
+                               const int64_t* slot_mapping,
+                               const int64_t* block_tables, int64_t table_width,
+                               const int64_t* positions,
+                               const void* q, const void* k, const void* v,
+                               int64_t q_token_stride, int64_t k_token_stride,
+                               int64_t v_token_stride,
+                               const void* q_weight, const void* k_weight,
+                               const void* cos, const void* sin,
+                               int64_t tokens, int64_t q_heads, float eps,
+                               int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,9 @@ SIGNATURES = {
     "mvme_paged_prefill_workspace_size": (_size, [_i64] * 8),
     "mvme_paged_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _size, _vp]),
+    "mvme_qk_norm_rope_write_kv": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp,
+                                          _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
+                                          ctypes.c_float, _int, _vp]),
 }
 
 

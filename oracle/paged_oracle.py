@@ -225,3 +225,56 @@ def prefill_metadata(token_sequences, block_tables, query_starts, block_size):
     padded = [t + [-1] * (width - len(t)) for t in clean]
     return {"positions": positions, "slot_mapping": slots, "cu_seqlens_q": offsets,
             "context_lens": contexts, "block_tables": padded}
+
+
+def rms_norm(x, weight, eps=1e-6):
+    """Qwen3 RMSNorm of the torch path (mini_engine/kernels/fallback.py:8-10).
+
+    fp32 mean of squares over the last dimension; the normalised value is cast
+    to the input dtype before the (low-precision) weight multiply.
+    """
+    variance = x.float().pow(2).mean(dim=-1, keepdim=True)
+    return (x.float() * torch.rsqrt(variance + eps)).to(x.dtype) * weight
+
+
+def apply_rope(q, k, cos, sin):
+    """Half-split rotary embedding of the torch path (mini_engine/kernels/fallback.py:13-20).
+
+    cos/sin are [tokens, 1, head_dim/2] (the torch branch unsqueezes them,
+    native_qwen3.py:153-154); every product is rounded to the tensor dtype
+    before the add/subtract, as eager fp16/bf16 arithmetic does.
+    """
+    half = q.shape[-1] // 2
+    q1, q2, k1, k2 = q[..., :half], q[..., half:], k[..., :half], k[..., half:]
+    return (torch.cat((q1 * cos - q2 * sin, q1 * sin + q2 * cos), dim=-1),
+            torch.cat((k1 * cos - k2 * sin, k1 * sin + k2 * cos), dim=-1))
+
+
+def qk_norm_rope_write_kv(q, k, v, q_weight, k_weight, cos, sin, key_cache, value_cache, *,
+                          slot_mapping=None, block_tables=None, positions=None, eps=1e-6):
+    """The four steps before paged attention in one call (torch data backend).
+
+    Attention._forward_prefill_batch (mini_engine/model/native_qwen3.py:150-157)
+    with a slot mapping, forward_decode_batch (:179-191) with block tables and
+    positions: q_norm/k_norm, apply_rope, then the KV write.  Writes the caches
+    in place and returns the rotated q.  Slots outside the cache and positions
+    outside the table are skipped (the HIP kernel's rule for metadata it does
+    not trust; the reference validates them away before this point).
+    """
+    q, k = rms_norm(q, q_weight, eps), rms_norm(k, k_weight, eps)
+    q, k = apply_rope(q, k, cos.unsqueeze(1), sin.unsqueeze(1))
+    num_blocks, block_size = key_cache.shape[:2]
+    if slot_mapping is not None:
+        slots = slot_mapping.tolist()
+    else:
+        slots = []
+        width = block_tables.shape[1]
+        for t, pos in enumerate(positions.tolist()):
+            page = int(block_tables[t, pos // block_size]) if 0 <= pos < width * block_size else -1
+            slots.append(page * block_size + pos % block_size if 0 <= page < num_blocks else -1)
+    keep = [t for t, slot in enumerate(slots) if 0 <= slot < num_blocks * block_size]
+    if keep:
+        index = torch.tensor(keep, dtype=torch.long)
+        write_kv_cache_slots(key_cache, value_cache, torch.tensor([slots[t] for t in keep], dtype=torch.long),
+                             k[index], v[index])
+    return q

@@ -159,3 +159,23 @@ def test_page_pool_shared_prefix_refcounts():
         pool.allocate("d", 4 * 20)
     with pytest.raises(ValueError, match="unallocated"):
         pool.allocate_with_prefix("e", 12, [a[2]])
+
+
+def test_fused_norm_rope_write_checks_before_any_launch():
+    from mini_engine_hip.kernels.rope import qk_norm_rope_write_kv
+    q, key, value, *_ = inputs()
+    k = v = torch.randn(8, 2, 16).half()
+    cos = sin = torch.ones(8, 8).half()
+    w = torch.ones(16).half()
+    slots = torch.arange(8, dtype=torch.int64)
+    with pytest.raises(ValueError, match="backend must be hip"):
+        qk_norm_rope_write_kv(q, k, v, w, w, cos, sin, key, value, slot_mapping=slots, backend="torch")
+    with pytest.raises(ValueError, match="either slot_mapping or block_tables"):
+        qk_norm_rope_write_kv(q, k, v, w, w, cos, sin, key, value)
+    with pytest.raises(ValueError, match="q and k must be"):
+        qk_norm_rope_write_kv(q, k[:, :, :8], v, w, w, cos, sin, key, value, slot_mapping=slots)
+    with pytest.raises(ValueError, match="FP16/BF16"):
+        qk_norm_rope_write_kv(q.float(), k.float(), v, w, w, cos, sin, key, value, slot_mapping=slots)
+    # CPU tensors are refused, never computed on the CPU.
+    with pytest.raises(RuntimeError, match="CUDA tensors"):
+        qk_norm_rope_write_kv(q, k, v, w, w, cos, sin, key, value, slot_mapping=slots)

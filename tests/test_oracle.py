@@ -356,3 +356,96 @@ def test_planted_prefill_mask_mistake_is_caught():
         out[begin:end] = F.scaled_dot_product_attention(q[begin:end].transpose(0, 1), key, value,
                                                         attn_mask=mask).transpose(0, 1)
     assert (out.double() - c_oracle.paged_prefill(q, kc, vc, offsets, starts, tables, lengths, 4)).abs().max() > 1e-3
+
+
+# --- fused q/k RMSNorm + RoPE + KV write --------------------------------------------------------
+
+def _f16_rope_loops(x, cos, sin):
+    """Per-element numpy float16 scalar arithmetic: every product and sum rounded to fp16."""
+    import numpy as np
+    x, cos, sin = (t.numpy() for t in (x, cos, sin))
+    half = x.shape[-1] // 2
+    out = np.empty_like(x)
+    for t in range(x.shape[0]):
+        for h in range(x.shape[1]):
+            for p in range(half):
+                a, b, c, s = x[t, h, p], x[t, h, p + half], cos[t, p], sin[t, p]
+                out[t, h, p] = np.float16(a * c) - np.float16(b * s)
+                out[t, h, p + half] = np.float16(a * s) + np.float16(b * c)
+    return torch.from_numpy(out)
+
+
+def _rope_case(seed=3, tokens=5, heads=4, kv_heads=2, dim=16, dtype=torch.float16):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(tokens, heads, dim, generator=gen).to(dtype)
+    k = torch.randn(tokens, kv_heads, dim, generator=gen).to(dtype)
+    angles = torch.randn(tokens, dim // 2, generator=gen) * 3
+    return q, k, angles.cos().to(dtype), angles.sin().to(dtype)
+
+
+def test_rope_identity_and_quarter_turn_closed_forms():
+    q, k, cos, sin = _rope_case()
+    ones, zeros = torch.ones_like(cos), torch.zeros_like(sin)
+    rq, rk = po.apply_rope(q, k, ones.unsqueeze(1), zeros.unsqueeze(1))
+    assert torch.equal(rq, q) and torch.equal(rk, k)
+    # cos = 0, sin = 1 rotates each (x1, x2) pair by 90 degrees: (-x2, x1).
+    rq, rk = po.apply_rope(q, k, zeros.unsqueeze(1), ones.unsqueeze(1))
+    assert torch.equal(rq, torch.cat((-q[..., 8:], q[..., :8]), -1))
+    assert torch.equal(rk, torch.cat((-k[..., 8:], k[..., :8]), -1))
+
+
+def test_rope_rounding_matches_float16_scalar_arithmetic():
+    q, k, cos, sin = _rope_case(seed=9)
+    rq, rk = po.apply_rope(q, k, cos.unsqueeze(1), sin.unsqueeze(1))
+    assert torch.equal(rq, _f16_rope_loops(q, cos, sin))
+    assert torch.equal(rk, _f16_rope_loops(k, cos, sin))
+    # Planted mistake: rounding only the finished sum (fp32 products) is not the reference's arithmetic.
+    half = 8
+    q1, q2 = q[..., :half].float(), q[..., half:].float()
+    c, s = cos.float().unsqueeze(1), sin.float().unsqueeze(1)
+    fused = torch.cat((q1 * c - q2 * s, q1 * s + q2 * c), -1).half()
+    assert not torch.equal(fused, rq)
+
+
+def test_rms_norm_constant_rows_and_float64():
+    dim = 16
+    weight = (torch.arange(dim, dtype=torch.float32) / 8 - 1).half()   # distinct per-element weights
+    # A constant row c normalises to sign(c) / sqrt(1 + eps / c^2): with eps = 3, c = 1 that is 1/2.
+    x = torch.ones(1, dim, dtype=torch.float16)
+    assert torch.equal(po.rms_norm(x, weight, eps=3.0)[0], (weight.float() * 0.5).half())
+    x = torch.full((1, dim), -2.0, dtype=torch.float16)
+    assert torch.equal(po.rms_norm(x, weight, eps=1e-6)[0], -weight)
+    # Random rows against a float64 restatement (mean, not sum; weight per element).
+    gen = torch.Generator().manual_seed(4)
+    x = (torch.randn(6, 3, dim, generator=gen) * 4).half()
+    x64 = x.double()
+    inv = 1 / torch.sqrt(x64.pow(2).mean(-1, keepdim=True) + 1e-6)
+    expected = (x64 * inv).half().double() * weight.double()
+    assert torch.allclose(po.rms_norm(x, weight).double(), expected, atol=2e-3, rtol=1e-3)
+    # Planted mistake: sum instead of mean fails the constant-row closed form.
+    wrong = (x[:1, 0].float() * torch.rsqrt(x[:1, 0].float().pow(2).sum(-1, keepdim=True) + 1e-6)).half() * weight
+    assert not torch.allclose(wrong.double(), expected[:1, 0], atol=2e-3, rtol=1e-3)
+
+
+def test_fused_oracle_writes_the_slots_of_the_batch_rules():
+    gen = torch.Generator().manual_seed(12)
+    tokens, heads, kv_heads, dim, block, pages = 4, 4, 2, 16, 4, 6
+    q, k, cos, sin = _rope_case(seed=12, tokens=tokens, heads=heads, kv_heads=kv_heads, dim=dim)
+    v = torch.randn(tokens, kv_heads, dim, generator=gen).half()
+    wq, wk = torch.rand(dim, generator=gen).half() + 0.5, torch.rand(dim, generator=gen).half() + 0.5
+    kc = torch.randn(pages, block, kv_heads, dim, generator=gen).half()
+    vc = torch.randn(pages, block, kv_heads, dim, generator=gen).half()
+    tables = torch.tensor([[3, 1], [0, 5], [2, 4], [-1, 1]], dtype=torch.int64)
+    positions = torch.tensor([5, 0, 9, 2], dtype=torch.int64)   # token 2 beyond capacity, token 3 on page -1
+    kd, vd = kc.clone(), vc.clone()
+    qd = po.qk_norm_rope_write_kv(q, k, v, wq, wk, cos, sin, kd, vd, block_tables=tables, positions=positions)
+    nq, nk = po.apply_rope(po.rms_norm(q, wq), po.rms_norm(k, wk), cos.unsqueeze(1), sin.unsqueeze(1))
+    assert torch.equal(qd, nq)
+    ke, ve = kc.clone(), vc.clone()
+    po.write_kv_cache_batch(ke, ve, tables[:2], positions[:2], nk[:2], v[:2], block)
+    assert torch.equal(kd, ke) and torch.equal(vd, ve)
+    # Slot mode: the same two rows through explicit slots, the invalid ones marked -1 / out of range.
+    ks, vs = kc.clone(), vc.clone()
+    slots = torch.tensor([1 * block + 1, 0, -1, pages * block], dtype=torch.int64)
+    qs = po.qk_norm_rope_write_kv(q, k, v, wq, wk, cos, sin, ks, vs, slot_mapping=slots)
+    assert torch.equal(qs, qd) and torch.equal(ks, kd) and torch.equal(vs, vd)
