@@ -13,26 +13,35 @@
 //   CUs; items of a query block that needs several chunks write fp32
 //   partials (unnormalised O, running max, running sum) that a merge kernel
 //   combines.  Items are enumerated densely from the metadata on the device,
-//   so grid position i is the i-th real item (work-groups past the end exit).
+//   so grid position i is the i-th real item (work-groups past the end exit);
+//   within a sequence the query blocks are enumerated from the last (longest
+//   key range) to the first, so that the work-groups dispatched last are the
+//   short ones.
 //
 //   K/V tiles of 64 keys move from the pages straight into LDS with
 //   global_load_lds_dwordx4 (no VGPR staging) into a ring of 4 stages, the
 //   copies running 3 tiles ahead of the tile being multiplied.  One barrier
 //   per tile both publishes the landed tile and retires the stage the next
 //   copy overwrites.  Each 256-byte key row is stored with its 16-byte
-//   chunks XOR-swizzled by the row index, which keeps both read patterns
-//   below free of bank conflicts.
+//   chunks XOR-swizzled by the row index, which keeps the K reads below free
+//   of bank conflicts (the transposing V reads still meet some).
 //
 //   Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32), so
-//   each lane holds the scores of ONE query row: the online softmax reduces
-//   across the four k-group lanes with permlane swaps, and the probabilities
-//   already sit in the B-operand layout of O^T = V^T P^T.  The V^T operand
-//   (8 consecutive keys of one dim per lane) is read from the row-major V
-//   tile with two ds_read_b64_tr_b16 transposing loads.  Keys are assigned to
-//   MFMA k-slots by one permutation applied to both operands.  Rescaling of
-//   the accumulators is deferred until a row maximum grows by more than
-//   2^8; tiles that are complete and entirely below the causal diagonal skip
-//   masking.  Accumulation, softmax and normalisation are fp32.
+//   each lane holds scores of ONE query row (four lanes share a row) and the
+//   probabilities already sit in the B-operand layout of O^T = V^T P^T.  The
+//   V^T operand (8 consecutive keys of one dim per lane) is read from the
+//   row-major V tile with two ds_read_b64_tr_b16 transposing loads.  Keys are
+//   assigned to MFMA k-slots by one permutation applied to both operands.
+//   The online softmax keeps a per-row reference m and computes
+//   p = 2^(s*scale - m) without a row maximum; the sum of a lane's 8
+//   probabilities of a half tile (which any probability above 2^8, inf or
+//   NaN pushes past 256) triggers the exact step: the row maximum across the
+//   four lanes (permlane swaps), a rescale of the accumulators, and new
+//   probabilities.  It runs when a row sees its first key and when a row's
+//   scores grow by several binary orders, so the accumulators are rescaled
+//   rarely and probabilities stay below 2^8.  Tiles that are complete and
+//   entirely below the causal diagonal skip masking.  Accumulation, softmax
+//   and normalisation are fp32.
 //
 // Generic path (any D <= 1024, any G): one wave per (query row, head),
 // online softmax over 64-key tiles, fp32 throughout.
@@ -155,7 +164,11 @@ __device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it
             it.qlen = __shfl(n, sel);
             it.start = __shfl(start, sel);
             it.ctx = __shfl(ctx, sel);
-            for (int64_t b0 = 0; b0 < it.qlen; b0 += a.qb) {
+            // Query blocks from the last (longest key range) to the first, so
+            // that the work-groups dispatched last are the short ones.
+            const int64_t nblocks = (it.qlen + a.qb - 1) / a.qb;
+            for (int64_t bi = nblocks - 1; bi >= 0; --bi) {
+                const int64_t b0 = bi * a.qb;
                 const int64_t e = block_kv_end(a, it.start, it.ctx, it.qlen, b0);
                 const int nc = chunks_of(a, e);
                 if (rem < nc) {
@@ -203,11 +216,11 @@ __device__ inline uint32_t lds_addr(P* p) {
 // LDS byte offset of 16-byte chunk `c` of key row `row` (XOR swizzle).
 __device__ inline int swz(int row, int c) { return row * kRowBytes + 16 * (c ^ (row & 15)); }
 
-// Row rescaling is deferred until a row's running max grows by more than
-// this many binary orders: probabilities stay below 2^kRescaleSlack, far
-// inside fp16/bf16/fp32 range, and the final division by the row sum makes
-// the result independent of the reference max.
-constexpr float kRescaleSlack = 8.f;
+// A lane's 8 probabilities of one half tile sum to at most this before the
+// row's reference is raised (some probability above 2^5 .. 2^8 triggers it):
+// probabilities stay far inside fp16/bf16/fp32 range, and the final division
+// by the row sum makes the result independent of the reference.
+constexpr float kPSumLimit = 256.f;
 
 // Full wait issued through the builtin, which the compiler's own wait
 // insertion understands (it then knows earlier loads have completed).
@@ -331,11 +344,15 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     wave_first = __builtin_amdgcn_readfirstlane(wave_first);
 
 
-    float m_run[kPfNb], l_part[kPfNb];
+    // m_run: the row's reference (log2 units, -inf until the row sees a key);
+    // nref = -m_run, or 0 while there is no reference (masked keys then give
+    // 2^-inf = 0 rather than NaN).
+    float m_run[kPfNb], nref[kPfNb], l_part[kPfNb];
     f32x4 o[kPfNb][8];
 #pragma unroll
     for (int nb = 0; nb < kPfNb; ++nb) {
         m_run[nb] = kNegInf;
+        nref[nb] = 0.f;
         l_part[nb] = 0.f;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) o[nb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -534,81 +551,77 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                         sc[nb][1] = T::mfma16x16x32(k1, qop[nb][dc], sc[nb][1]);
                     }
                 }
-                // Row maxima over the 32 keys (log2 units).
-                float mx[kPfNb];
-                if (fast) {
-#pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) {
-                        float r = sc[nb][0][0];
-#pragma unroll
-                        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) r = fmaxf(r, sc[nb][kk][j]);
-                        mx[nb] = row4_max(r) * a.scale_log2;
-                    }
-                } else {
+                // Scores -> probabilities against the running reference m_run.
+                // Fast tiles keep raw scores and scale inside the exponent;
+                // edge tiles are scaled, biased and masked in place first.
+                if (!fast) {
 #pragma unroll
                     for (int nb = 0; nb < kPfNb; ++nb) {
                         const int lim = pos[nb] - tile0 - 32 * h - 4 * lg;  // key (16*kk + j) must be <= lim
-                        float r = kNegInf;
 #pragma unroll
                         for (int kk = 0; kk < 2; ++kk) {
                             const f32x4 bias = *reinterpret_cast<const f32x4*>(&smb[32 * h + 16 * kk + 4 * lg]);
 #pragma unroll
                             for (int j = 0; j < 4; ++j) {
-                                float v = sc[nb][kk][j] * a.scale_log2 + bias[j];
-                                if (16 * kk + j > lim) v = kNegInf;
-                                sc[nb][kk][j] = v;
-                                r = fmaxf(r, v);
+                                const float v = sc[nb][kk][j] * a.scale_log2 + bias[j];
+                                sc[nb][kk][j] = 16 * kk + j > lim ? kNegInf : v;
                             }
                         }
-                        mx[nb] = row4_max(r);
                     }
                 }
-                // Deferred rescale: only when some row's max outgrew its reference.
-                bool grow = false;
+                const float mult = fast ? a.scale_log2 : 1.f;
+                // No row maximum on the common path: the reference only has to
+                // keep every probability small, which the sum of a lane's
+                // probabilities checks after the fact (inf and NaN included).
+                float p[kPfNb][8], dl[kPfNb];
+                bool need = false;
 #pragma unroll
-                for (int nb = 0; nb < kPfNb; ++nb) grow = grow || mx[nb] > m_run[nb] + kRescaleSlack;
-                if (__builtin_amdgcn_ballot_w64(grow)) {
+                for (int nb = 0; nb < kPfNb; ++nb) {
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            p[nb][4 * kk + j] = fast_exp2(fmaf(sc[nb][kk][j], mult, nref[nb]));
+                    dl[nb] = ((p[nb][0] + p[nb][1]) + (p[nb][2] + p[nb][3])) +
+                             ((p[nb][4] + p[nb][5]) + (p[nb][6] + p[nb][7]));
+                    // A row without a reference yet needs one as soon as it
+                    // sees a key (key 32h of the tile is at or before its position).
+                    need = need | !(dl[nb] <= kPSumLimit) | ((m_run[nb] == kNegInf) & (pos[nb] >= tile0 + 32 * h));
+                }
+                if (__builtin_amdgcn_ballot_w64(need)) {
+                    // Exact step: row maxima over the 4 lanes of each row,
+                    // rescale what is accumulated, recompute the probabilities.
 #pragma unroll
                     for (int nb = 0; nb < kPfNb; ++nb) {
-                        const float mn = fmaxf(m_run[nb], mx[nb]);
+                        float r = kNegInf;
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) r = fmaxf(r, sc[nb][kk][j] * mult);
+                        const float mn = fmaxf(m_run[nb], row4_max(r));
                         const float alpha = mn == kNegInf ? 1.f : fast_exp2(m_run[nb] - mn);
                         m_run[nb] = mn;
                         l_part[nb] *= alpha;
 #pragma unroll
                         for (int dt = 0; dt < 8; ++dt) o[nb][dt] *= alpha;
+                        nref[nb] = mn == kNegInf ? 0.f : -mn;
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                p[nb][4 * kk + j] = fast_exp2(fmaf(sc[nb][kk][j], mult, nref[nb]));
+                        dl[nb] = ((p[nb][0] + p[nb][1]) + (p[nb][2] + p[nb][3])) +
+                                 ((p[nb][4] + p[nb][5]) + (p[nb][6] + p[nb][7]));
                     }
                 }
-                // Probabilities, packed as the B operand of the PV products:
+                // Packed as the B operand of the PV products:
                 // k-slot 4*kk + j <-> key 32h + 16kk + 4*lg + j.
                 u32x4 pop[kPfNb];
-                if (fast) {
 #pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) {
-                        const float nref = m_run[nb] == kNegInf ? 0.f : -m_run[nb];
-                        float p[8];
-#pragma unroll
-                        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) p[4 * kk + j] = fast_exp2(fmaf(sc[nb][kk][j], a.scale_log2, nref));
-                        l_part[nb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-                        pop[nb] = u32x4{T::pack(p[0], p[1]), T::pack(p[2], p[3]), T::pack(p[4], p[5]),
-                                        T::pack(p[6], p[7])};
-                    }
-                } else {
-#pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) {
-                        const float ref = m_run[nb] == kNegInf ? 0.f : m_run[nb];
-                        float p[8];
-#pragma unroll
-                        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) p[4 * kk + j] = fast_exp2(sc[nb][kk][j] - ref);
-                        l_part[nb] += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-                        pop[nb] = u32x4{T::pack(p[0], p[1]), T::pack(p[2], p[3]), T::pack(p[4], p[5]),
-                                        T::pack(p[6], p[7])};
-                    }
+                for (int nb = 0; nb < kPfNb; ++nb) {
+                    l_part[nb] += dl[nb];
+                    pop[nb] = u32x4{T::pack(p[nb][0], p[nb][1]), T::pack(p[nb][2], p[nb][3]),
+                                    T::pack(p[nb][4], p[nb][5]), T::pack(p[nb][6], p[nb][7])};
                 }
                 // O^T += V^T P^T for these 32 keys; V^T operand by transposing reads.
 #pragma unroll
