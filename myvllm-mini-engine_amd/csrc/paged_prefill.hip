@@ -10,19 +10,20 @@
 //   pairs that share every K/V tile; each of the 8 waves (two per SIMD) owns
 //   32 rows (two 16-row MFMA column blocks).  Long contexts with few query
 //   blocks are cut into key chunks so that the work items spread over all
-//   CUs; items of a query block that needs several chunks write fp32
-//   partials (unnormalised O, running max, running sum) that a merge kernel
-//   combines.  Items are enumerated densely from the metadata on the device,
+//   CUs; items of a query block that needs several chunks write partials
+//   (the output normalised by its own probability sum -- bf16 for bf16
+//   inputs, fp32 for fp16 -- with the fp32 reference and sum) that a merge
+//   kernel combines.  Items are enumerated densely from the metadata on the device,
 //   so grid position i is the i-th real item (work-groups past the end exit);
 //   within a sequence the query blocks are enumerated from the last (longest
 //   key range) to the first, so that the work-groups dispatched last are the
 //   short ones.
 //
 //   K/V tiles of 64 keys move from the pages straight into LDS with
-//   global_load_lds_dwordx4 (no VGPR staging) into a ring of 4 stages, the
-//   copies running 3 tiles ahead of the tile being multiplied.  One barrier
-//   per tile both publishes the landed tile and retires the stage the next
-//   copy overwrites.  Each 256-byte key row is stored with its 16-byte
+//   global_load_lds_dwordx4 (no VGPR staging) into a ring of 4 stages, in
+//   pairs: one barrier per pair of tiles both publishes the two landed tiles
+//   and retires the previous pair's stages, which the copies of the next
+//   pair (issued right after the barrier) overwrite.  Each 256-byte key row is stored with its 16-byte
 //   chunks XOR-swizzled by the row index, which keeps the K reads below free
 //   of bank conflicts (the transposing V reads still meet some).
 //
@@ -32,6 +33,10 @@
 //   V^T operand (8 consecutive keys of one dim per lane) is read from the
 //   row-major V tile with two ds_read_b64_tr_b16 transposing loads.  Keys are
 //   assigned to MFMA k-slots by one permutation applied to both operands.
+//   Every accumulator takes its products back to back (the four d-slices of
+//   a score block; both halves of a tile for an output block): the matrix
+//   core forwards a result into the next product of the same accumulator,
+//   while alternating accumulators costs issue slots.
 //   The online softmax keeps a per-row reference m and computes
 //   p = 2^(s*scale - m) without a row maximum; the sum of a lane's 8
 //   probabilities of a half tile (which any probability above 2^8, inf or
@@ -57,7 +62,6 @@ constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfNb = 2;                        // 16-row MFMA column blocks per wave
 constexpr int kPfRows = kPfWaves * kPfNb * 16;  // 256 query rows per work-group (32 per wave)
 constexpr int kPfStages = 4;                    // LDS ring of K/V tiles
-constexpr int kPfAhead = kPfStages - 1;         // tiles in flight ahead of the one computed
 constexpr int kPfIpw = 16 / kPfWaves;           // 1 KiB copy instructions per wave per K (or V) tile
 constexpr int kPfKeys = 64;        // keys per LDS tile
 constexpr int kPfD = 128;
@@ -80,7 +84,7 @@ struct PrefillArgs {
     const int64_t* starts;
     const int64_t* tables;
     const int64_t* lens;
-    float* ws_o;   // [T, Hq, max_chunks, D] unnormalised partial outputs
+    void* ws_o;    // [T, Hq, max_chunks, D] partial outputs normalised by their sum (PartialOf<T>)
     float* ws_ml;  // [T, Hq, max_chunks, 2] (running max in log2 units, sum)
     int* ws_tok;   // [T] chunks of the token's query block (written by its chunk-0 items)
     int item_stride;  // 0: one item per work-group; else items walked per work-group
@@ -124,6 +128,12 @@ __device__ inline int seq_items(const PrefillArgs& a, int64_t n, int64_t start, 
     return count;
 }
 
+// Element type of the key-chunk partial outputs.  They are normalised by
+// their own probability sum (a convex combination of V rows), so bf16 keeps
+// them as accurately as the bf16 output; fp16 inputs keep fp32 partials.
+template <typename T> struct PartialOf { using type = float; };
+template <> struct PartialOf<BFloat16> { using type = uint16_t; };
+
 struct PrefillItem {
     int seq, q0, chunk, nchunks;
     int64_t kv_end;
@@ -135,9 +145,10 @@ struct PrefillItem {
 // counts its items, a wave prefix sum locates the sequence, the lane that
 // owns it hands its metadata over by shuffles, and that one sequence's query
 // blocks are walked.  Every wave of the work-group computes the same answer.
-__device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it) {
+__device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it, int* total_items = nullptr) {
     const int lane = __lane_id();
     int base = 0;
+    bool found = false;
     for (int s0 = 0; s0 < a.num_seqs; s0 += kWave) {
         const int s = s0 + lane;
         int64_t row0 = 0, n = 0, start = 0, ctx = 0;
@@ -155,7 +166,7 @@ __device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it
             if (lane >= off) incl += other;
         }
         const int total = __shfl(incl, kWave - 1);
-        if (item < base + total) {
+        if (!found && item >= base && item < base + total) {
             const uint64_t hit = __ballot(base + incl > item);
             const int sel = __builtin_ctzll(hit);
             it.seq = s0 + sel;
@@ -176,15 +187,17 @@ __device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it
                     it.chunk = rem;
                     it.kv_end = e;
                     it.nchunks = nc;
-                    return true;
+                    found = true;
+                    break;
                 }
                 rem -= nc;
             }
-            return false;  // unreachable when the counts are consistent
+            if (!total_items) return found;  // (not found only if the counts are inconsistent)
         }
         base += total;
     }
-    return false;
+    if (total_items) *total_items = base;
+    return found;
 }
 
 // Direct global -> LDS copy of 16 bytes per lane: lane i's bytes land at LDS
@@ -461,10 +474,10 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 
     // Page ids of the first tiles (scalar loads) go out before the Q loads
     // so that both latencies overlap.
-    int pro_pg[kPfAhead + 1];
+    int pro_pg[2];
     if constexpr (PAGES == kPagesPerTile) {
 #pragma unroll
-        for (int k = 0; k <= kPfAhead; ++k) {
+        for (int k = 0; k < 2; ++k) {
             lookup(t_begin + k);
             pro_pg[k] = pg_next[0];
         }
@@ -483,12 +496,10 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     }
     wait_vmcnt_all();
 
-    // Prologue: tiles t_begin .. t_begin+kPfAhead-1 in flight (copies of
-    // tiles past the chunk read zeros into stages nobody computes on, which
-    // keeps the per-iteration copy count constant).
+    // Prologue: the first pair of tiles in flight.
     if (t_begin < t_end) {
 #pragma unroll
-        for (int k = 0; k < kPfAhead; ++k) {
+        for (int k = 0; k < 2; ++k) {
             if constexpr (PAGES == kPagesPerTile) {
 #pragma unroll
                 for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pro_pg[k];
@@ -497,114 +508,89 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             }
             issue(t_begin + k, k);
         }
-        if constexpr (PAGES == kPagesPerTile) {
-#pragma unroll
-            for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pro_pg[kPfAhead];
-        } else {
-            lookup(t_begin + kPfAhead);
-        }
     }
-    int st = kPfStages - 1;  // ring position of `tile` (advanced at the top of the loop)
-    for (int tile = t_begin; tile < t_end; ++tile) {
-        st = (st + 1) & (kPfStages - 1);
-        // Tile `tile` has landed for this lane when at most the copies of the
-        // later tiles in flight are outstanding; the barrier makes every
-        // lane's copies visible.  It also proves every wave has finished (and
-        // received all LDS reads of) the previous tile, whose stage the copy
-        // below refills (a ring of kPfStages stages with copies kPfStages-1
-        // tiles ahead): one barrier per tile.
-        if constexpr (SCALAR_PAGES) {
-            static_assert(2 * kPfIpw * (kPfAhead - 1) == 8, "vmcnt immediate below");
-            asm volatile("s_waitcnt vmcnt(8) lgkmcnt(0)\n\ts_barrier" : : : "memory");
-        } else {
-            dma_landed_barrier();
+    for (int tp = t_begin; tp < t_end; tp += 2) {
+        const int st0 = (tp - t_begin) & (kPfStages - 1);
+        // Both tiles of the pair have landed (this lane's copies, then every
+        // lane's through the barrier), and every wave is done with the
+        // previous pair, whose stages the copies below refill.
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            lookup(tp + 2 + k);
+            issue(tp + 2 + k, (st0 + 2 + k) & (kPfStages - 1));
         }
-        issue(tile + kPfAhead, (st + kPfAhead) & (kPfStages - 1));
-        lookup(tile + kPfAhead + 1);
-        const int tile0 = tile * kPfKeys;
-        if (tile0 <= wave_last) {
-            const uint8_t* smk = &sm_k[st][0];
-            const float* smb = &sm_b[st][0];
-            // Every key of the tile present and visible to every row of the
-            // wave: no bias and no causal mask needed.
-            static_assert(kPfWaves == 8, "two int4 flag reads below");
-            const int4 fa = *reinterpret_cast<const int4*>(&sm_full[st][0]);
-            const int4 fb = *reinterpret_cast<const int4*>(&sm_full[st][4]);
-            const bool fast = (fa.x & fa.y & fa.z & fa.w & fb.x & fb.y & fb.z & fb.w) &&
-                              tile0 + kPfKeys - 1 <= wave_first;
-            typedef __attribute__((address_space(3))) uint8_t lds_u8;
-            lds_u8* vbase = (lds_u8*)&sm_v[st][0];
-            // Two halves of 32 keys: S^T -> softmax -> O^T += V^T P^T each.
+        for (int k = 0; k < 2 && tp + k < t_end; ++k) {
+            const int tile = tp + k;
+            const int st = (st0 + k) & (kPfStages - 1);
+            const int tile0 = tile * kPfKeys;
+            if (tile0 <= wave_last) {
+                const uint8_t* smk = &sm_k[st][0];
+                const float* smb = &sm_b[st][0];
+                // Every key of the tile present and visible to every row of the
+                // wave: no bias and no causal mask needed.
+                static_assert(kPfWaves == 8, "two int4 flag reads below");
+                const int4 fa = *reinterpret_cast<const int4*>(&sm_full[st][0]);
+                const int4 fb = *reinterpret_cast<const int4*>(&sm_full[st][4]);
+                const bool fast = (fa.x & fa.y & fa.z & fa.w & fb.x & fb.y & fb.z & fb.w) &&
+                                  tile0 + kPfKeys - 1 <= wave_first;
+                typedef __attribute__((address_space(3))) uint8_t lds_u8;
+                lds_u8* vbase = (lds_u8*)&sm_v[st][0];
+                // Two halves of 32 keys: S^T -> probabilities each, then
+                // O^T += V^T P^T over the whole tile, two products back to back
+                // per accumulator.
+                u32x4 pops[2][kPfNb];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                // S^T = K Q^T for key sub-tiles 2h, 2h+1: 8 independent accumulators.
-                f32x4 sc[kPfNb][2];
+                for (int h = 0; h < 2; ++h) {
+                    // S^T = K Q^T for key sub-tiles 2h, 2h+1: 8 independent accumulators.
+                    f32x4 sc[kPfNb][2];
 #pragma unroll
-                for (int nb = 0; nb < kPfNb; ++nb) sc[nb][0] = sc[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int nb = 0; nb < kPfNb; ++nb) sc[nb][0] = sc[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    // Each accumulator takes its four products back to back: the
+                    // matrix core forwards a result straight into the next
+                    // product of the same accumulator, while alternating between
+                    // accumulators costs issue slots.
+                    u32x4 kop[2][4];
 #pragma unroll
-                for (int dc = 0; dc < 4; ++dc) {
-                    const u32x4 k0 = *reinterpret_cast<const u32x4*>(smk + 32 * h * kRowBytes + koff[dc]);
-                    const u32x4 k1 = *reinterpret_cast<const u32x4*>(smk + (32 * h + 16) * kRowBytes + koff[dc]);
-#pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) {
-                        sc[nb][0] = T::mfma16x16x32(k0, qop[nb][dc], sc[nb][0]);
-                        sc[nb][1] = T::mfma16x16x32(k1, qop[nb][dc], sc[nb][1]);
+                    for (int dc = 0; dc < 4; ++dc) {
+                        kop[0][dc] = *reinterpret_cast<const u32x4*>(smk + 32 * h * kRowBytes + koff[dc]);
+                        kop[1][dc] = *reinterpret_cast<const u32x4*>(smk + (32 * h + 16) * kRowBytes + koff[dc]);
                     }
-                }
-                // Scores -> probabilities against the running reference m_run.
-                // Fast tiles keep raw scores and scale inside the exponent;
-                // edge tiles are scaled, biased and masked in place first.
-                if (!fast) {
-#pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) {
-                        const int lim = pos[nb] - tile0 - 32 * h - 4 * lg;  // key (16*kk + j) must be <= lim
-#pragma unroll
-                        for (int kk = 0; kk < 2; ++kk) {
-                            const f32x4 bias = *reinterpret_cast<const f32x4*>(&smb[32 * h + 16 * kk + 4 * lg]);
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) {
-                                const float v = sc[nb][kk][j] * a.scale_log2 + bias[j];
-                                sc[nb][kk][j] = 16 * kk + j > lim ? kNegInf : v;
-                            }
-                        }
-                    }
-                }
-                const float mult = fast ? a.scale_log2 : 1.f;
-                // No row maximum on the common path: the reference only has to
-                // keep every probability small, which the sum of a lane's
-                // probabilities checks after the fact (inf and NaN included).
-                float p[kPfNb][8], dl[kPfNb];
-                bool need = false;
-#pragma unroll
-                for (int nb = 0; nb < kPfNb; ++nb) {
 #pragma unroll
                     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-                        for (int j = 0; j < 4; ++j)
-                            p[nb][4 * kk + j] = fast_exp2(fmaf(sc[nb][kk][j], mult, nref[nb]));
-                    dl[nb] = ((p[nb][0] + p[nb][1]) + (p[nb][2] + p[nb][3])) +
-                             ((p[nb][4] + p[nb][5]) + (p[nb][6] + p[nb][7]));
-                    // A row without a reference yet needs one as soon as it
-                    // sees a key (key 32h of the tile is at or before its position).
-                    need = need | !(dl[nb] <= kPSumLimit) | ((m_run[nb] == kNegInf) & (pos[nb] >= tile0 + 32 * h));
-                }
-                if (__builtin_amdgcn_ballot_w64(need)) {
-                    // Exact step: row maxima over the 4 lanes of each row,
-                    // rescale what is accumulated, recompute the probabilities.
+                        for (int nb = 0; nb < kPfNb; ++nb) {
+#pragma unroll
+                            for (int dc = 0; dc < 4; ++dc)
+                                sc[nb][kk] = T::mfma16x16x32(kop[kk][dc], qop[nb][dc], sc[nb][kk]);
+                            __builtin_amdgcn_sched_barrier(0);  // keep the chain contiguous
+                        }
+                    // Scores -> probabilities against the running reference m_run.
+                    // Fast tiles keep raw scores and scale inside the exponent;
+                    // edge tiles are scaled, biased and masked in place first.
+                    if (!fast) {
+#pragma unroll
+                        for (int nb = 0; nb < kPfNb; ++nb) {
+                            const int lim = pos[nb] - tile0 - 32 * h - 4 * lg;  // key (16*kk + j) must be <= lim
+#pragma unroll
+                            for (int kk = 0; kk < 2; ++kk) {
+                                const f32x4 bias = *reinterpret_cast<const f32x4*>(&smb[32 * h + 16 * kk + 4 * lg]);
+#pragma unroll
+                                for (int j = 0; j < 4; ++j) {
+                                    const float v = sc[nb][kk][j] * a.scale_log2 + bias[j];
+                                    sc[nb][kk][j] = 16 * kk + j > lim ? kNegInf : v;
+                                }
+                            }
+                        }
+                    }
+                    const float mult = fast ? a.scale_log2 : 1.f;
+                    // No row maximum on the common path: the reference only has to
+                    // keep every probability small, which the sum of a lane's
+                    // probabilities checks after the fact (inf and NaN included).
+                    float p[kPfNb][8], dl[kPfNb];
+                    bool need = false;
 #pragma unroll
                     for (int nb = 0; nb < kPfNb; ++nb) {
-                        float r = kNegInf;
-#pragma unroll
-                        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                            for (int j = 0; j < 4; ++j) r = fmaxf(r, sc[nb][kk][j] * mult);
-                        const float mn = fmaxf(m_run[nb], row4_max(r));
-                        const float alpha = mn == kNegInf ? 1.f : fast_exp2(m_run[nb] - mn);
-                        m_run[nb] = mn;
-                        l_part[nb] *= alpha;
-#pragma unroll
-                        for (int dt = 0; dt < 8; ++dt) o[nb][dt] *= alpha;
-                        nref[nb] = mn == kNegInf ? 0.f : -mn;
 #pragma unroll
                         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -612,29 +598,79 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                                 p[nb][4 * kk + j] = fast_exp2(fmaf(sc[nb][kk][j], mult, nref[nb]));
                         dl[nb] = ((p[nb][0] + p[nb][1]) + (p[nb][2] + p[nb][3])) +
                                  ((p[nb][4] + p[nb][5]) + (p[nb][6] + p[nb][7]));
+                        // A row without a reference yet needs one as soon as it
+                        // sees a key (key 32h of the tile is at or before its position).
+                        need = need | !(dl[nb] <= kPSumLimit) | ((m_run[nb] == kNegInf) & (pos[nb] >= tile0 + 32 * h));
+                    }
+                    if (__builtin_amdgcn_ballot_w64(need)) {
+                        // Exact step: row maxima over the 4 lanes of each row,
+                        // rescale what is accumulated, recompute the probabilities.
+#pragma unroll
+                        for (int nb = 0; nb < kPfNb; ++nb) {
+                            float r = kNegInf;
+#pragma unroll
+                            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                                for (int j = 0; j < 4; ++j) r = fmaxf(r, sc[nb][kk][j] * mult);
+                            const float mn = fmaxf(m_run[nb], row4_max(r));
+                            const float alpha = mn == kNegInf ? 1.f : fast_exp2(m_run[nb] - mn);
+                            m_run[nb] = mn;
+                            l_part[nb] *= alpha;
+#pragma unroll
+                            for (int dt = 0; dt < 8; ++dt) o[nb][dt] *= alpha;
+                            if (h == 1) {
+                                // The first half's products are still to be accumulated.
+#pragma unroll
+                                for (int w = 0; w < 4; ++w)
+                                    pops[0][nb][w] =
+                                        T::pack(T::lo(pops[0][nb][w]) * alpha, T::hi(pops[0][nb][w]) * alpha);
+                            }
+                            nref[nb] = mn == kNegInf ? 0.f : -mn;
+#pragma unroll
+                            for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                                for (int j = 0; j < 4; ++j)
+                                    p[nb][4 * kk + j] = fast_exp2(fmaf(sc[nb][kk][j], mult, nref[nb]));
+                            dl[nb] = ((p[nb][0] + p[nb][1]) + (p[nb][2] + p[nb][3])) +
+                                     ((p[nb][4] + p[nb][5]) + (p[nb][6] + p[nb][7]));
+                        }
+                    }
+                    // Packed as the B operand of the PV products:
+                    // k-slot 4*kk + j <-> key 32h + 16kk + 4*lg + j.
+#pragma unroll
+                    for (int nb = 0; nb < kPfNb; ++nb) {
+                        l_part[nb] += dl[nb];
+                        pops[h][nb] = u32x4{T::pack(p[nb][0], p[nb][1]), T::pack(p[nb][2], p[nb][3]),
+                                            T::pack(p[nb][4], p[nb][5]), T::pack(p[nb][6], p[nb][7])};
                     }
                 }
-                // Packed as the B operand of the PV products:
-                // k-slot 4*kk + j <-> key 32h + 16kk + 4*lg + j.
-                u32x4 pop[kPfNb];
+                // O^T += V^T P^T over the tile; V^T operands by transposing reads,
+                // one dim block ahead of the products that use them.
+                auto vread = [&](int dt, u32x4 (&vop)[2]) __attribute__((always_inline)) {
 #pragma unroll
-                for (int nb = 0; nb < kPfNb; ++nb) {
-                    l_part[nb] += dl[nb];
-                    pop[nb] = u32x4{T::pack(p[nb][0], p[nb][1]), T::pack(p[nb][2], p[nb][3]),
-                                    T::pack(p[nb][4], p[nb][5]), T::pack(p[nb][6], p[nb][7])};
-                }
-                // O^T += V^T P^T for these 32 keys; V^T operand by transposing reads.
+                    for (int h = 0; h < 2; ++h) {
+                        const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (lds_s16x4*)(vbase + 32 * h * kRowBytes + voff[dt]));
+                        const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (lds_s16x4*)(vbase + (32 * h + 16) * kRowBytes + voff[dt]));
+                        const u32x2 w0 = __builtin_bit_cast(u32x2, t0);
+                        const u32x2 w1 = __builtin_bit_cast(u32x2, t1);
+                        vop[h] = u32x4{w0[0], w0[1], w1[0], w1[1]};
+                    }
+                };
+                u32x4 vcur[2], vnext[2];
+                vread(0, vcur);
 #pragma unroll
                 for (int dt = 0; dt < 8; ++dt) {
-                    const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4*)(vbase + 32 * h * kRowBytes + voff[dt]));
-                    const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (lds_s16x4*)(vbase + (32 * h + 16) * kRowBytes + voff[dt]));
-                    const u32x2 w0 = __builtin_bit_cast(u32x2, t0);
-                    const u32x2 w1 = __builtin_bit_cast(u32x2, t1);
-                    const u32x4 vop = {w0[0], w0[1], w1[0], w1[1]};
+                    if (dt + 1 < 8) vread(dt + 1, vnext);
 #pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) o[nb][dt] = T::mfma16x16x32(vop, pop[nb], o[nb][dt]);
+                    for (int nb = 0; nb < kPfNb; ++nb) {
+                        o[nb][dt] = T::mfma16x16x32(vcur[0], pops[0][nb], o[nb][dt]);
+                        o[nb][dt] = T::mfma16x16x32(vcur[1], pops[1][nb], o[nb][dt]);
+                        __builtin_amdgcn_sched_barrier(0);  // keep the two products back to back
+                    }
+                    vcur[0] = vnext[0];
+                    vcur[1] = vnext[1];
                 }
             }
         }
@@ -658,9 +694,19 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             }
         } else {
             const int64_t slot = rowid * a.max_chunks + chunk;
-            float* po = a.ws_o + slot * kPfD;
+            const float inv = (row_ok[nb] && l_row > 0.f) ? 1.f / l_row : 0.f;
+            using P = typename PartialOf<T>::type;
+            P* po = static_cast<P*>(a.ws_o) + slot * kPfD;
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lg) = o[nb][dt];
+            for (int dt = 0; dt < 8; ++dt) {
+                if constexpr (sizeof(P) == 4) {
+                    *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lg) = o[nb][dt] * inv;
+                } else {
+                    const u32x2 w = {T::pack(o[nb][dt][0] * inv, o[nb][dt][1] * inv),
+                                     T::pack(o[nb][dt][2] * inv, o[nb][dt][3] * inv)};
+                    *reinterpret_cast<u32x2*>(po + 16 * dt + 4 * lg) = w;
+                }
+            }
             if (lg == 0) {
                 a.ws_ml[slot * 2] = row_ok[nb] ? m_run[nb] : kNegInf;
                 a.ws_ml[slot * 2 + 1] = row_ok[nb] ? l_row : 0.f;
@@ -674,11 +720,11 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     }
 }
 
-// Items are enumerated densely, so the first index past the end ends a
-// work-group's walk.  WALK = false: one item per work-group (the grid covers
-// every possible item).  WALK = true: one work-group per CU slot, each
-// walking items idx, idx + item_stride, ... (a separate instantiation, so
-// that the one-item kernel keeps its register allocation).
+// Items are enumerated densely.  WALK = false: one item per work-group (the
+// grid covers every possible item; work-groups past the end exit).  WALK =
+// true: one work-group per CU slot, each walking items idx, idx +
+// item_stride, ... below the item count (a separate instantiation, so that
+// the one-item kernel keeps its register allocation).
 template <typename T, int PAGES, bool WALK>
 __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) PrefillLds lds;
@@ -687,17 +733,25 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
         if (!find_item(a, blockIdx.x / a.kv_heads, item)) return;
         prefill_item<T, PAGES>(a, item, lds);
     } else {
-        for (int idx = blockIdx.x / a.kv_heads;; idx += a.item_stride) {
-            PrefillItem item;
-            if (!find_item(a, idx, item)) return;
+        // The first lookup also counts the items, so that the walk ends
+        // without a lookup past the end.
+        int total = 0;
+        int idx = blockIdx.x / a.kv_heads;
+        PrefillItem item;
+        bool ok = find_item(a, idx, item, &total);
+        while (ok) {
             prefill_item<T, PAGES>(a, item, lds);
+            idx += a.item_stride;
+            if (idx >= total) break;
             __syncthreads();  // every wave is done with the LDS ring before the next item refills it
+            ok = find_item(a, idx, item);
         }
     }
 }
 
 // Combines the key-chunk partials of rows whose query block needed several
-// chunks: out = sum_c O_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
+// chunks: with o_c the chunk's normalised output, l_c its probability sum and
+// m_c its reference, out = sum_c w_c o_c / sum_c w_c, w_c = l_c 2^(m_c - M).
 // One work-group per packed token (its chunk count comes from the attention
 // kernel); thread t handles head t/16, dims 8*(t%16) .. +8.
 constexpr int kMergeThreads = 256;
@@ -709,42 +763,54 @@ __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(Pref
     // item; the clamp keeps reads inside the workspace for any other value.
     const int nchunks = min(a.ws_tok[token], a.max_chunks);
     if (nchunks <= 1) return;
-    constexpr int kGroup = 4;  // chunks whose partials are loaded together
+    constexpr int kGroup = 8;  // chunks whose partials are loaded together
     for (int idx = threadIdx.x; idx < a.q_heads * (kPfD / 8); idx += kMergeThreads) {
         const int head = idx / (kPfD / 8);
         const int d0 = 8 * (idx % (kPfD / 8));
         const int64_t slot0 = (token * a.q_heads + head) * a.max_chunks;
-        const float* ml = a.ws_ml + slot0 * 2;
-        float mx = kNegInf;
-        for (int c0 = 0; c0 < nchunks; c0 += kGroup) {
-#pragma unroll
-            for (int k = 0; k < kGroup; ++k)
-                if (c0 + k < nchunks) mx = fmaxf(mx, ml[2 * (c0 + k)]);
-        }
-        const float ref = mx == kNegInf ? 0.f : mx;
-        float sum = 0.f;
+        const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + slot0;
+        // One pass: every load of a group of chunks is in flight together,
+        // and the running reference moves (with a rescale) only when a
+        // group holds a larger maximum.
+        float mref = kNegInf, sum = 0.f;
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         for (int c0 = 0; c0 < nchunks; c0 += kGroup) {
-            // All loads of the group first, so that they are in flight together.
+            using P = typename PartialOf<T>::type;
             f32x4 x[kGroup][2];
-            float mc[kGroup], lc[kGroup];
+            float2 mlc[kGroup];
 #pragma unroll
             for (int k = 0; k < kGroup; ++k) {
                 x[k][0] = x[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-                mc[k] = kNegInf;
-                lc[k] = 0.f;
+                mlc[k] = float2{kNegInf, 0.f};
                 if (c0 + k < nchunks) {
-                    const f32x4* po = reinterpret_cast<const f32x4*>(a.ws_o + (slot0 + c0 + k) * kPfD + d0);
-                    x[k][0] = po[0];
-                    x[k][1] = po[1];
-                    mc[k] = ml[2 * (c0 + k)];
-                    lc[k] = ml[2 * (c0 + k) + 1];
+                    const P* po = static_cast<const P*>(a.ws_o) + (slot0 + c0 + k) * kPfD + d0;
+                    if constexpr (sizeof(P) == 4) {
+                        x[k][0] = reinterpret_cast<const f32x4*>(po)[0];
+                        x[k][1] = reinterpret_cast<const f32x4*>(po)[1];
+                    } else {
+                        const u32x4 w = *reinterpret_cast<const u32x4*>(po);
+                        x[k][0] = f32x4{T::lo(w[0]), T::hi(w[0]), T::lo(w[1]), T::hi(w[1])};
+                        x[k][1] = f32x4{T::lo(w[2]), T::hi(w[2]), T::lo(w[3]), T::hi(w[3])};
+                    }
+                    mlc[k] = ml[c0 + k];
                 }
             }
+            float gmax = kNegInf;
+#pragma unroll
+            for (int k = 0; k < kGroup; ++k) gmax = fmaxf(gmax, mlc[k].x);
+            if (gmax > mref) {
+                const float scale = mref == kNegInf ? 0.f : fast_exp2(mref - gmax);
+                sum *= scale;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[i] *= scale;
+                mref = gmax;
+            }
+            const float ref = mref == kNegInf ? 0.f : mref;
 #pragma unroll
             for (int k = 0; k < kGroup; ++k) {
-                const float w = mc[k] == kNegInf ? 0.f : fast_exp2(mc[k] - ref);
-                sum = fmaf(lc[k], w, sum);
+                // Chunk weight: its probability sum at the common reference.
+                const float w = mlc[k].x == kNegInf ? 0.f : mlc[k].y * fast_exp2(mlc[k].x - ref);
+                sum += w;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     acc[i] = fmaf(x[k][0][i], w, acc[i]);
@@ -892,7 +958,7 @@ constexpr int64_t kPrefillCUs = 256;
 // Host plan from shapes only (lengths stay on the device).  Enough query
 // blocks to occupy the GPU twice over: no key split.  Otherwise split the
 // keys into chunks of at least 512 (and at most 16 chunks per block), which
-// spreads long contexts over all CUs at the cost of fp32 partials.
+// spreads long contexts over all CUs at the cost of partials and a merge.
 PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64_t kv_heads,
                               int64_t head_dim, int64_t block_size, int64_t table_width, int64_t chunk_tokens) {
     PrefillPlan p{};
@@ -985,8 +1051,8 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         a.chunk = p.chunk;
         a.max_chunks = p.max_chunks;
         if (need > 0) {
-            a.ws_o = static_cast<float*>(workspace);
-            a.ws_ml = a.ws_o + total_tokens * q_heads * p.max_chunks * kPfD;
+            a.ws_o = workspace;
+            a.ws_ml = static_cast<float*>(workspace) + total_tokens * q_heads * p.max_chunks * kPfD;
             a.ws_tok = reinterpret_cast<int*>(a.ws_ml + total_tokens * q_heads * p.max_chunks * 2);
         }
         // The item count depends on lengths that stay on the device, so the
