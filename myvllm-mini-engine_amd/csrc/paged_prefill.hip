@@ -482,8 +482,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             pro_pg[k] = pg_next[0];
         }
     }
-    // Q^T operands: row (nb, li), d = 32*dc + 8*lg .. +8.  Loaded (and waited
-    // for) before any tile copy is issued, so the copies own the counter.
+    // Q^T operands: row (nb, li), d = 32*dc + 8*lg .. +8.  Their latency
+    // overlaps the first pair's copies: the first pair barrier waits for the
+    // whole vector-memory counter.
     u32x4 qop[kPfNb][4];
 #pragma unroll
     for (int nb = 0; nb < kPfNb; ++nb) {
@@ -494,7 +495,6 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             if (row_ok[nb]) qop[nb][dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
         }
     }
-    wait_vmcnt_all();
 
     // Prologue: the first pair of tiles in flight.
     if (t_begin < t_end) {
