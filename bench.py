@@ -199,7 +199,7 @@ def cpu_baseline(layers, oracle, torch, budget_s):
 # Other workloads of the path (reported under "extra").
 # ---------------------------------------------------------------------------
 
-EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "norm_rope")
+EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "norm_rope", "after_attention")
 
 
 def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, oracle,
@@ -216,6 +216,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, oracle, dev, extra)
     if "norm_rope" in names:
         _extra_norm_rope(torch, oracle, dev, extra)
+    if "after_attention" in names:
+        _extra_after_attention(torch, oracle, dev, extra)
     return extra
 
 
@@ -405,6 +407,42 @@ def _extra_norm_rope(torch, oracle, dev, extra):
             "q_bit_identical_frac": (out.cpu() == want_q).float().mean().item(),
             "k_max_abs_error": max_abs(got_k, want_k),
             "v_bit_exact": bool(torch.equal(vc.cpu().view(-1, HKV, D)[rows], vc_o.view(-1, HKV, D)[rows]))}
+
+
+def _extra_after_attention(torch, oracle, dev, extra):
+    """The step after attention at the headline batch: o_proj GEMV (a library GEMM, hipBLASLt
+    through torch.mm, as the reference's CudaLinear uses cuBLAS) and greedy argmax over a
+    151,936-entry vocabulary (the HIP kernel), 32 sequences, hidden 2048."""
+    from mini_engine_hip.sampling import greedy_argmax
+
+    batch, hidden, vocab = BATCH, 2048, 151936
+    gen = torch.Generator().manual_seed(BASE_SEED + 11)
+    attn = torch.randn(batch, HQ * D, generator=gen).to(torch.bfloat16).to(dev)
+    w_t = (torch.randn(HQ * D, hidden, generator=gen) * 0.02).to(torch.bfloat16).to(dev)   # o_proj.weight^T
+    out_o = torch.empty(batch, hidden, dtype=torch.bfloat16, device=dev)
+
+    def many(fn, n):
+        def run():
+            for _ in range(n):
+                fn()
+        return run
+    ms, _ = graph_time_ms(many(lambda: torch.mm(attn, w_t, out=out_o), 50), torch, calls_per_graph=50,
+                          replays=20, warmup=3)
+    o_bytes = HQ * D * hidden * 2 + batch * HQ * D * 2 + batch * hidden * 2
+    o_ref = attn.float().cpu() @ w_t.float().cpu()
+    extra["o_proj_gemv_b32_2048x2048_bf16"] = {
+        "us_per_call": ms / 50 * 1e3, "GBps": o_bytes / (ms / 50 * 1e-3) / 1e9, "library": "hipBLASLt (torch.mm)",
+        "max_abs_error_vs_fp32": max_abs(out_o, o_ref)}
+    for dtype, name in ((torch.bfloat16, "greedy_argmax_b32_vocab151936_bf16"),
+                        (torch.float32, "greedy_argmax_b32_vocab151936_fp32")):
+        logits = torch.randn(batch, vocab, generator=gen).to(dtype).to(dev)
+        tokens = torch.empty(batch, dtype=torch.int64, device=dev)
+        ms, _ = graph_time_ms(many(lambda: greedy_argmax(logits, out=tokens), 50), torch, calls_per_graph=50,
+                              replays=20, warmup=3)
+        moved = batch * vocab * logits.element_size() + batch * 8
+        extra[name] = {"us_per_call": ms / 50 * 1e3, "GBps": moved / (ms / 50 * 1e-3) / 1e9,
+                       "frac_of_hbm_peak": moved / (ms / 50 * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                       "tokens_equal_oracle": bool(torch.equal(tokens.cpu(), oracle.greedy_argmax(logits.cpu())))}
 
 
 def main(argv=None):

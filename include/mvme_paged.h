@@ -35,8 +35,8 @@ extern "C" {
 
 #define MVME_ABI_VERSION 1
 
-/* Element types of the KV cache, queries and outputs. */
-enum mvme_dtype { MVME_FP16 = 0, MVME_BF16 = 1 };
+/* Element types of the KV cache, queries and outputs (FP32: sampling logits only). */
+enum mvme_dtype { MVME_FP16 = 0, MVME_BF16 = 1, MVME_FP32 = 2 };
 
 /* Status codes. */
 enum mvme_status { MVME_OK = 0, MVME_EINVAL = 1, MVME_ELAUNCH = 2, MVME_EWORKSPACE = 3 };
@@ -217,6 +217,28 @@ int mvme_qk_norm_rope_write_kv(void* q_out, void* key_cache, void* value_cache,
                                const void* cos, const void* sin,
                                int64_t tokens, int64_t q_heads, float eps,
                                int dtype, void* stream);
+
+/*
+ * Bytes of device workspace mvme_greedy_argmax needs (0 when every row is
+ * reduced by one work-group).  Pure host function.
+ */
+size_t mvme_greedy_argmax_workspace_size(int64_t batch, int64_t vocab);
+
+/*
+ * Greedy sampling: out[b] = argmax over v < vocab of logits[b * row_stride + v]
+ * for b < batch (<= 65535), with torch.argmax's ranking (largest value; ties
+ * and NaNs resolve to the lowest index, NaN above every number).  dtype:
+ * MVME_FP16, MVME_BF16 or MVME_FP32.  `workspace` (8-byte aligned) holds
+ * mvme_greedy_argmax_workspace_size(batch, vocab) bytes of per-slice partial
+ * results.  batch = 0 is a no-op.
+ * Replaces: greedy_argmax_cuda / partial_argmax + final_argmax
+ *   (mini_engine/kernels/csrc/sampling.cu:1-68), bound as
+ *   extension.greedy_argmax (csrc/bindings.cpp:186-193) and called from
+ *   sample_next_token(..., backend="cuda") (mini_engine/sampling.py:4-17).
+ */
+int mvme_greedy_argmax(int64_t* out, const void* logits, int64_t batch, int64_t vocab,
+                       int64_t row_stride, int dtype, void* workspace, size_t workspace_bytes,
+                       void* stream);
 
 #ifdef __cplusplus
 }

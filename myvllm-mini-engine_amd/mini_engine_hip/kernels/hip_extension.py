@@ -14,7 +14,7 @@ import torch
 
 from .. import build as _build
 
-FP16, BF16 = 0, 1
+FP16, BF16, FP32 = 0, 1, 2
 OK, EINVAL, ELAUNCH, EWORKSPACE = 0, 1, 2, 3
 ABI_VERSION = 1
 
@@ -41,6 +41,8 @@ SIGNATURES = {
     "mvme_qk_norm_rope_write_kv": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp,
                                           _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
                                           ctypes.c_float, _int, _vp]),
+    "mvme_greedy_argmax_workspace_size": (_size, [_i64, _i64]),
+    "mvme_greedy_argmax": (_int, [_vp, _vp, _i64, _i64, _i64, _int, _vp, _size, _vp]),
 }
 
 
@@ -72,6 +74,9 @@ class HipLibrary:
 
     def prefill_workspace_size(self, *args) -> int:
         return int(self._lib.mvme_paged_prefill_workspace_size(*args))
+
+    def argmax_workspace_size(self, *args) -> int:
+        return int(self._lib.mvme_greedy_argmax_workspace_size(*args))
 
 
 @functools.lru_cache(maxsize=1)

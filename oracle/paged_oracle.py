@@ -278,3 +278,8 @@ def qk_norm_rope_write_kv(q, k, v, q_weight, k_weight, cos, sin, key_cache, valu
         write_kv_cache_slots(key_cache, value_cache, torch.tensor([slots[t] for t in keep], dtype=torch.long),
                              k[index], v[index])
     return q
+
+
+def greedy_argmax(logits):
+    """Greedy sampler of the torch path (mini_engine/sampling.py:22-23): torch.argmax per row."""
+    return logits.argmax(dim=-1)

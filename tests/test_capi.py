@@ -30,7 +30,7 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     symbols = declared_symbols()
-    assert len(symbols) == 11
+    assert len(symbols) == 13
     raw = ctypes.CDLL(str(hip_build.library_path()))
     for name in symbols:
         assert hasattr(raw, name), name
@@ -113,3 +113,18 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
             ext.load_hip_extension()
     finally:
         ext.load_hip_extension.cache_clear()
+
+
+def test_argmax_workspace_plan(lib):
+    # Enough slices per row to cover the CUs twice (>= 2048 elements each), a single slice otherwise.
+    assert lib.argmax_workspace_size(32, 151936) == 32 * 16 * 8
+    assert lib.argmax_workspace_size(1, 151936) == 75 * 8
+    assert lib.argmax_workspace_size(600, 151936) == 0
+    assert lib.argmax_workspace_size(5, 1) == 0
+    assert lib.argmax_workspace_size(0, 10) == 0
+    status = lib._lib.mvme_greedy_argmax(None, None, 32, 151936, 151936, 1, None, 0, None)
+    assert status == ext.EINVAL
+    status = lib._lib.mvme_greedy_argmax(1, 1, 32, 151936, 151936, 1, None, 0, None)
+    assert status == ext.EWORKSPACE and "workspace" in lib.last_error()
+    assert lib._lib.mvme_greedy_argmax(1, 1, 2, 10, 9, 1, None, 0, None) == ext.EINVAL
+    assert lib._lib.mvme_greedy_argmax(1, 1, 2, 10, 10, 7, None, 0, None) == ext.EINVAL

@@ -179,3 +179,16 @@ def test_fused_norm_rope_write_checks_before_any_launch():
     # CPU tensors are refused, never computed on the CPU.
     with pytest.raises(RuntimeError, match="CUDA tensors"):
         qk_norm_rope_write_kv(q, k, v, w, w, cos, sin, key, value, slot_mapping=slots)
+
+
+def test_greedy_sampling_contract_on_cpu():
+    from mini_engine_hip.sampling import sample_next_token
+    x = torch.randn(2, 9)
+    with pytest.raises(ValueError, match="sampling backend must be hip"):
+        sample_next_token(x, backend="torch")
+    with pytest.raises(ValueError, match="greedy temperature=0"):
+        sample_next_token(x, temperature=0.7)
+    with pytest.raises(ValueError, match="logits must have shape"):
+        sample_next_token(x[0])
+    with pytest.raises(RuntimeError, match="contiguous CUDA"):
+        sample_next_token(x)

@@ -449,3 +449,35 @@ def test_fused_oracle_writes_the_slots_of_the_batch_rules():
     slots = torch.tensor([1 * block + 1, 0, -1, pages * block], dtype=torch.int64)
     qs = po.qk_norm_rope_write_kv(q, k, v, wq, wk, cos, sin, ks, vs, slot_mapping=slots)
     assert torch.equal(qs, qd) and torch.equal(ks, kd) and torch.equal(vs, vd)
+
+
+# --- greedy sampling ------------------------------------------------------------------------------
+
+def _argmax_loops(x):
+    """First NaN of a row, else the first index of its maximum (-0.0 == +0.0)."""
+    out = []
+    for row in x.float().tolist():
+        nan = [i for i, v in enumerate(row) if v != v]
+        if nan:
+            out.append(nan[0])
+            continue
+        best = max(row)
+        out.append(next(i for i, v in enumerate(row) if v == best))
+    return torch.tensor(out, dtype=torch.int64)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("vocab", [1, 257, 4097])
+def test_greedy_oracle_ties_nan_inf_and_tail(dtype, vocab):
+    """The reference's sampling cases (tests/test_cuda_sampling.py:16-25) against plain loops."""
+    gen = torch.Generator().manual_seed(29)
+    x = torch.randn(6, vocab, generator=gen).to(dtype)
+    x[0].fill_(float("-inf"))
+    x[1].fill_(1)
+    x[2, -1] = float("inf")
+    x[3, -1] = float("nan")
+    x[3, 0] = float("nan")
+    x[4, -1] = 99
+    x[5].fill_(0)
+    x[5, vocab // 2:] = -0.0
+    assert torch.equal(po.greedy_argmax(x), _argmax_loops(x))
