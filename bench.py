@@ -163,6 +163,67 @@ def decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_at
             "passed": scatter_ok and err <= 2e-3}
 
 
+def decode_attention_block_step(args, torch, layers, paged_attention, oracle):
+    """The attention block of the decode step for all 28 headline layers in one captured graph:
+    per layer the fused q/k RMSNorm + RoPE + KV page write of the new token (replacing q_norm,
+    k_norm, apply_rope and write_kv_cache_batch, native_qwen3.py:179-191), paged attention over
+    the updated context, and the o_proj GEMV (hipBLASLt through torch.mm; native_qwen3.py:197).
+    Inputs are synthetic QKV projections of the batch; reuses the headline layers' caches."""
+    from mini_engine_hip.kernels.rope import qk_norm_rope_write_kv
+
+    hidden = 2048
+    gen = torch.Generator(device="cuda").manual_seed(BASE_SEED + 99)
+    for c in layers:
+        c["qkv"] = torch.randn((BATCH, (HQ + 2 * HKV) * D), generator=gen, device="cuda").half()
+        c["wq"] = (torch.rand((D,), generator=gen, device="cuda") + 0.5).half()
+        c["wk"] = (torch.rand((D,), generator=gen, device="cuda") + 0.5).half()
+        angles = torch.randn((BATCH, D // 2), generator=gen, device="cuda")
+        c["cos"], c["sin"] = angles.cos().half(), angles.sin().half()
+        c["w_o"] = (torch.randn((HQ * D, hidden), generator=gen, device="cuda") * 0.02).half()
+        c["positions"] = (c["context_lens"] - 1).contiguous()
+        c["q_rot"] = torch.empty((BATCH, HQ, D), dtype=torch.float16, device="cuda")
+        c["hidden"] = torch.empty((BATCH, hidden), dtype=torch.float16, device="cuda")
+
+    def split(c):
+        q = c["qkv"][:, :HQ * D].view(BATCH, HQ, D)
+        k = c["qkv"][:, HQ * D:(HQ + HKV) * D].view(BATCH, HKV, D)
+        v = c["qkv"][:, (HQ + HKV) * D:].view(BATCH, HKV, D)
+        return q, k, v
+
+    def step():
+        for c in layers:
+            q, k, v = split(c)
+            qk_norm_rope_write_kv(q, k, v, c["wq"], c["wk"], c["cos"], c["sin"], c["key_cache"], c["value_cache"],
+                                  block_tables=c["block_tables"], positions=c["positions"], validate=False,
+                                  out=c["q_rot"])
+            paged_attention(c["q_rot"], c["key_cache"], c["value_cache"], c["block_tables"], c["context_lens"],
+                            BLOCK, backend="hip", validate=False, out=c["out"])
+            torch.mm(c["out"].view(BATCH, HQ * D), c["w_o"], out=c["hidden"])
+
+    ms, _ = graph_time_ms(step, torch, calls_per_graph=3 * LAYERS, replays=args.steps, warmup=args.warmup)
+    # Layer 0 against the oracle: the rotated q, the written K/V rows, attention, o_proj.
+    c = layers[0]
+    q, k, v = (t.cpu() for t in split(c))
+    tables, positions = c["block_tables"].cpu(), c["positions"].cpu()
+    kc, vc = c["key_cache"].cpu(), c["value_cache"].cpu()
+    kc_o, vc_o = kc.clone(), vc.clone()
+    q_ref = oracle.qk_norm_rope_write_kv(q, k, v, c["wq"].cpu(), c["wk"].cpu(), c["cos"].cpu(), c["sin"].cpu(),
+                                         kc_o, vc_o, block_tables=tables, positions=positions)
+    rope_err = max(max_abs(c["q_rot"], q_ref), max_abs(kc, kc_o))
+    v_exact = torch.equal(vc, vc_o)
+    tensors = {"query": c["q_rot"].cpu(), "key_cache": kc, "value_cache": vc, "block_tables": tables,
+               "context_lens": c["context_lens"].cpu()}
+    attn_err = max_abs(c["out"], oracle.fp32_oracle(tensors, BLOCK))
+    o_err = max_abs(c["hidden"], c["out"].float().cpu().view(BATCH, -1) @ c["w_o"].float().cpu())
+    passed = v_exact and rope_err <= 4e-3 and attn_err <= 2e-3 and o_err <= 2e-2
+    for c in layers:
+        for key in ("qkv", "wq", "wk", "cos", "sin", "w_o", "positions", "q_rot", "hidden"):
+            del c[key]
+    return {"us_per_step": ms * 1e3, "us_per_layer": ms * 1e3 / LAYERS, "launches_per_step": 3 * LAYERS,
+            "v_rows_bit_exact": v_exact, "max_abs_error_rope_layer0": rope_err,
+            "max_abs_error_attention_layer0": attn_err, "max_abs_error_o_proj_layer0": o_err, "passed": passed}
+
+
 def cpu_baseline(layers, oracle, torch, budget_s):
     """The reference's torch decode path, restated in the oracle, on host cores."""
     threads = torch.get_num_threads()
@@ -501,11 +562,13 @@ def main(argv=None):
     log(f"headline: {step_ms:.3f} ms/step, {per_call_ms * 1e3:.2f} us/call, {achieved_gbs:.0f} GB/s")
     parity = headline_parity(layers, paged_oracle)
     log(f"parity: {parity}")
-    decode_step = None
+    decode_step = attention_block = None
     if not args.no_extra:
         decode_step = decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_attention,
                                                paged_oracle)
         log(f"decode step with scatter: {decode_step}")
+        attention_block = decode_attention_block_step(args, torch, layers, paged_attention, paged_oracle)
+        log(f"decode attention block: {attention_block}")
 
     traffic = None
     traffic_file = ROOT / "profiles" / "paged_decode_b32_ctx2048_traffic.txt"
@@ -546,6 +609,7 @@ def main(argv=None):
         result["extra"] = extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention,
                                           workloads, paged_oracle, names=tuple(args.extra.split(",")))
         result["extra"]["decode_step_b32_ctx2048_28layers_with_scatter"] = decode_step
+        result["extra"]["decode_attention_block_b32_ctx2048_28layers"] = attention_block
         log(f"extra: {json.dumps(result['extra'])}")
     if not args.no_cpu_baseline:
         gen_layers = [workloads.decode_b32_layer(torch.device("cuda:0"), seed=BASE_SEED + 2)]
