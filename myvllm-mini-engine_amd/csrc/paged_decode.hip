@@ -54,6 +54,7 @@ struct DecodeArgs {
     int gtiles;     // group / G
     int64_t num_blocks;
     int block_size;
+    int block_shift;  // log2(block_size) when it is a power of two, else -1
     int table_width;
     int capacity;   // table_width * block_size
     int partition;  // tokens per partition (multiple of the wave tile)
@@ -119,24 +120,54 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     const uint16_t* vbase = static_cast<const uint16_t*>(a.value_cache) + kvh * D + 8 * c;
     const int64_t* table = a.tables + (int64_t)b * a.table_width;
 
-    for (int it = start + wave * S::kTpi; it < end; it += kStep) {
+    // Page-uniform iterations: the iteration's tokens lie in one page, whose
+    // id is a scalar load issued one iteration ahead (its latency hides
+    // behind the current iteration); the loads are a scalar page base plus
+    // 32-bit per-lane offsets, with no per-load branches.
+    typedef __attribute__((address_space(4))) const int64_t const_i64;
+    const const_i64* ctable = (const const_i64*)table;
+    const int row_bytes = (int)(row_elems * 2);
+    uint32_t lane_off[L];
+#pragma unroll
+    for (int u = 0; u < L; ++u) lane_off[u] = (uint32_t)((u * S::kTpl + tl) * row_bytes + (kvh * D + 8 * c) * 2);
+    auto page_of = [&](int t) __attribute__((always_inline)) -> int64_t {
+        if (t >= end) return -1;
+        return ctable[a.block_shift >= 0 ? t >> a.block_shift : t / a.block_size];
+    };
+    int it = __builtin_amdgcn_readfirstlane(start + wave * S::kTpi);
+    int64_t page_next = 0;
+    if constexpr (PAGE_UNIFORM) page_next = page_of(it);
+    for (; it < end; it += kStep) {
         u32x4 kk[L], vv[L];
         bool ok[L];
         if constexpr (PAGE_UNIFORM) {
-            // The whole iteration lies inside one page: one scalar lookup.
-            const int64_t page = table[it / a.block_size];
+            const int64_t page = page_next;
+            page_next = page_of(it + kStep);
             const bool page_ok = page >= 0 && page < a.num_blocks;
-            const int64_t base = page * page_elems + (int64_t)(it % a.block_size) * row_elems;
+            const int in_page = a.block_shift >= 0 ? it & (a.block_size - 1) : it % a.block_size;
 #pragma unroll
             for (int u = 0; u < L; ++u) {
-                const int slot = u * S::kTpl + tl;
-                ok[u] = page_ok && it + slot < end;
-                const int64_t off = base + slot * row_elems;
+                ok[u] = page_ok && it + u * S::kTpl + tl < end;
                 kk[u] = vv[u] = u32x4{0u, 0u, 0u, 0u};
-                if (ok[u] && chunk_ok) {
-                    kk[u] = *reinterpret_cast<const u32x4*>(kbase + off);
-                    vv[u] = *reinterpret_cast<const u32x4*>(vbase + off);
+            }
+            if (page_ok) {  // wave-uniform
+                const int64_t base = (page * a.block_size + in_page) * (int64_t)row_bytes;
+                const uint8_t* kp = static_cast<const uint8_t*>(a.key_cache) + base;
+                const uint8_t* vp = static_cast<const uint8_t*>(a.value_cache) + base;
+#pragma unroll
+                for (int u = 0; u < L; ++u) {
+                    // In-page rows past the context are loaded (in bounds) and zeroed below.
+                    if constexpr (S::kChunks == S::kLpt) {
+                        kk[u] = *reinterpret_cast<const u32x4*>(kp + lane_off[u]);
+                        vv[u] = *reinterpret_cast<const u32x4*>(vp + lane_off[u]);
+                    } else if (chunk_ok) {
+                        kk[u] = *reinterpret_cast<const u32x4*>(kp + lane_off[u]);
+                        vv[u] = *reinterpret_cast<const u32x4*>(vp + lane_off[u]);
+                    }
                 }
+#pragma unroll
+                for (int u = 0; u < L; ++u)
+                    if (!ok[u]) vv[u] = u32x4{0u, 0u, 0u, 0u};  // 0 * (stale NaN) must not reach acc
             }
         } else {
 #pragma unroll
@@ -454,6 +485,7 @@ extern "C" int mvme_paged_attention(void* out, const void* query, const void* ke
     a.gtiles = (int)(group / p.gtile);
     a.num_blocks = num_blocks;
     a.block_size = (int)block_size;
+    a.block_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctzll((unsigned long long)block_size) : -1;
     a.table_width = (int)table_width;
     a.capacity = (int)(table_width * block_size);
     a.partition = p.partition;
