@@ -24,8 +24,9 @@
 //   pairs: one barrier per pair of tiles both publishes the two landed tiles
 //   and retires the previous pair's stages, which the copies of the next
 //   pair (issued right after the barrier) overwrite.  Each 256-byte key row is stored with its 16-byte
-//   chunks XOR-swizzled by the row index, which keeps the K reads below free
-//   of bank conflicts (the transposing V reads still meet some).
+//   chunks XOR-swizzled by the row index (K) or twice the row index (V),
+//   which keeps both the K reads and the transposing V reads below free of
+//   bank conflicts.
 //
 //   Scores are computed transposed, S^T = K Q^T (v_mfma_f32_16x16x32), so
 //   each lane holds scores of ONE query row (four lanes share a row) and the
@@ -226,9 +227,6 @@ __device__ inline uint32_t lds_addr(P* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)p;
 }
 
-// LDS byte offset of 16-byte chunk `c` of key row `row` (XOR swizzle).
-__device__ inline int swz(int row, int c) { return row * kRowBytes + 16 * (c ^ (row & 15)); }
-
 // A lane's 8 probabilities of one half tile sum to at most this before the
 // row's reference is raised (some probability above 2^5 .. 2^8 triggers it):
 // probabilities stay far inside fp16/bf16/fp32 range, and the final division
@@ -373,7 +371,10 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 
     // Swizzled LDS offsets this lane reads (independent of the tile):
     // K chunk 4*dc + lg of row 16*kt + li, and the transposing V reads of
-    // rows 32*c + 4*lg + li/4 (+16), dims 16*dt + 4*(li%4) .. +4.
+    // rows 32*c + 4*lg + li/4 (+16), dims 16*dt + 4*(li%4) .. +4.  K rows
+    // store global chunk c in slot c ^ (row & 15); V rows in slot
+    // c ^ (2*row & 15), so that the 16 lanes of a transposing read (4 rows x
+    // 2 adjacent chunks) hit 8 different 16-byte bank groups.
     int koff[4];
 #pragma unroll
     for (int dc = 0; dc < 4; ++dc) koff[dc] = li * kRowBytes + 16 * ((4 * dc + lg) ^ li);
@@ -381,22 +382,24 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     int voff[8];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt)
-        voff[dt] = vrow * kRowBytes + 16 * ((2 * dt + ((li & 3) >> 1)) ^ (vrow & 15)) + 8 * (li & 1);
+        voff[dt] = vrow * kRowBytes + 16 * ((2 * dt + ((li & 3) >> 1)) ^ ((2 * vrow) & 15)) + 8 * (li & 1);
 
     // Copy plan: a tile's K (and V) is 16 instructions of 1 KiB; wave w issues
     // instructions j = kPfIpw*w + i, each covering key rows 4j..4j+3 (lane ->
-    // row 4j + lane/16, LDS slot lane%16 = global chunk (lane%16)^(row&15)).
+    // row 4j + lane/16, LDS slot lane%16 = global chunk (lane%16)^(row&15) for
+    // K, (lane%16)^(2*row&15) for V).
     const int64_t row_bytes_g = (int64_t)a.kv_heads * kPfD * 2;
     const int64_t page_bytes_g = (int64_t)a.block_size * row_bytes_g;
     const uint8_t* kcache = static_cast<const uint8_t*>(a.key_cache) + (int64_t)kvh * kPfD * 2;
     const uint8_t* vcache = static_cast<const uint8_t*>(a.value_cache) + (int64_t)kvh * kPfD * 2;
     const int bs_shift = a.block_shift;
     const int lrow = lane >> 4;  // row inside the instruction's 4 rows
-    uint32_t tile_off[kPfIpw];   // per-lane byte offset of a whole-tile copy from the tile's row 0
+    uint32_t tile_off[kPfIpw], tile_off_v[kPfIpw];  // per-lane byte offsets of whole-tile copies from row 0
 #pragma unroll
     for (int i = 0; i < kPfIpw; ++i) {
         const int row = 4 * (kPfIpw * wave + i) + lrow;
         tile_off[i] = (uint32_t)(row * row_bytes_g) + 16u * (uint32_t)((lane & 15) ^ (row & 15));
+        tile_off_v[i] = (uint32_t)(row * row_bytes_g) + 16u * (uint32_t)((lane & 15) ^ ((2 * row) & 15));
     }
 
     // The table is read-only here: reading it through the constant address
@@ -438,7 +441,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 for (int i = 0; i < kPfIpw; ++i) {
                     const int j = kPfIpw * wave + i;
                     lds_dma16_s(kcache + base, tile_off[i], lk + 1024 * j);
-                    lds_dma16_s(vcache + base, tile_off[i], lv + 1024 * j);
+                    lds_dma16_s(vcache + base, tile_off_v[i], lv + 1024 * j);
                     if ((lane & 15) == 0) sm_b[st][4 * j + lrow] = 0.f;
                 }
                 if (lane == 0) sm_full[st][wave] = 1;
@@ -452,6 +455,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             const int row = 4 * j + lrow;
             const int key = tile * kPfKeys + row;
             const int cidx = (lane & 15) ^ (row & 15);
+            const int cidx_v = (lane & 15) ^ ((2 * row) & 15);
             const int page = pg_next[i];
             // Rows past the chunk inside a valid first-row page are masked too.
             const bool ok = page >= 0 && key < chunk_end;
@@ -460,9 +464,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             const uint8_t* gv = gk;
             if (ok) {
                 const int in_page = bs_shift >= 0 ? key & (a.block_size - 1) : key % a.block_size;
-                const int64_t off = (int64_t)page * page_bytes_g + (int64_t)in_page * row_bytes_g + 16 * cidx;
-                gk = kcache + off;
-                gv = vcache + off;
+                const int64_t off = (int64_t)page * page_bytes_g + (int64_t)in_page * row_bytes_g;
+                gk = kcache + off + 16 * cidx;
+                gv = vcache + off + 16 * cidx_v;
             }
             lds_dma16(gk, lds_addr(&sm_k[st][0]) + 1024 * j);
             lds_dma16(gv, lds_addr(&sm_v[st][0]) + 1024 * j);
