@@ -206,12 +206,10 @@ __device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it
 // Issued as inline assembly so that the compiler does not serialise it
 // against unrelated LDS reads; the kernel orders it with explicit
 // s_waitcnt vmcnt(0) + s_barrier before the destination stage is read.
-// M0 is saved and restored around the copy.
+// M0 is declared clobbered (the compiler sets it again where it needs it).
 __device__ inline void lds_dma16(const void* gptr, uint32_t lds_base) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved) : "v"(gptr), "s"(base));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(base) : "m0");
 }
 
 // Wave-wide waits + work-group barrier with a compiler memory fence.
@@ -254,15 +252,15 @@ __device__ inline float row4_sum(float x) {
 
 // Direct global -> LDS copy from a wave-uniform base plus a per-lane 32-bit
 // byte offset (the SGPR-base form of global_load_lds_dwordx4: no 64-bit
-// per-lane address arithmetic).
+// per-lane address arithmetic).  M0 (the LDS destination) is declared
+// clobbered instead of saved and restored: the compiler sets it again where
+// it needs it.
 __device__ inline void lds_dma16_s(const uint8_t* sbase, uint32_t voff, uint32_t lds_base) {
     const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);
     const uint64_t g = (uint64_t)(uintptr_t)sbase;
     const uint64_t gu = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(g >> 32)) << 32) |
                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)g);
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved) : "v"(voff), "s"(gu), "s"(base));
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(gu), "s"(base) : "m0");
 }
 
 constexpr int kPagesPerLane = 0;
@@ -442,7 +440,6 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     const int j = kPfIpw * wave + i;
                     lds_dma16_s(kcache + base, tile_off[i], lk + 1024 * j);
                     lds_dma16_s(vcache + base, tile_off_v[i], lv + 1024 * j);
-                    if ((lane & 15) == 0) sm_b[st][4 * j + lrow] = 0.f;
                 }
                 if (lane == 0) sm_full[st][wave] = 1;
                 return;
@@ -536,8 +533,8 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 static_assert(kPfWaves == 8, "two int4 flag reads below");
                 const int4 fa = *reinterpret_cast<const int4*>(&sm_full[st][0]);
                 const int4 fb = *reinterpret_cast<const int4*>(&sm_full[st][4]);
-                const bool fast = (fa.x & fa.y & fa.z & fa.w & fb.x & fb.y & fb.z & fb.w) &&
-                                  tile0 + kPfKeys - 1 <= wave_first;
+                const bool full = (fa.x & fa.y & fa.z & fa.w & fb.x & fb.y & fb.z & fb.w) != 0;
+                const bool fast = full && tile0 + kPfKeys - 1 <= wave_first;
                 typedef __attribute__((address_space(3))) uint8_t lds_u8;
                 lds_u8* vbase = (lds_u8*)&sm_v[st][0];
                 // Two halves of 32 keys: S^T -> probabilities each, then
@@ -578,7 +575,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                             const int lim = pos[nb] - tile0 - 32 * h - 4 * lg;  // key (16*kk + j) must be <= lim
 #pragma unroll
                             for (int kk = 0; kk < 2; ++kk) {
-                                const f32x4 bias = *reinterpret_cast<const f32x4*>(&smb[32 * h + 16 * kk + 4 * lg]);
+                                // Full tiles leave the bias unwritten: every key row is present.
+                                const f32x4 bias = full ? f32x4{0.f, 0.f, 0.f, 0.f}
+                                                        : *reinterpret_cast<const f32x4*>(&smb[32 * h + 16 * kk + 4 * lg]);
 #pragma unroll
                                 for (int j = 0; j < 4; ++j) {
                                     const float v = sc[nb][kk][j] * a.scale_log2 + bias[j];
