@@ -59,6 +59,7 @@ struct DecodeArgs {
     int capacity;   // table_width * block_size
     int partition;  // tokens per partition (multiple of the wave tile)
     int max_parts;
+    int lpt_batch;  // batch size when units go longest sequence first (<= 64), else 0
     float scale_log2;
 };
 
@@ -82,12 +83,38 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     const int unit = blockIdx.x;
     const int part = blockIdx.y;
     const int per_seq = a.kv_heads * a.gtiles;
-    const int b = unit / per_seq;
+    int b = unit / per_seq;
     const int r = unit - b * per_seq;
+    int len;
+    if (a.lpt_batch > 0) {
+        // Whole-sequence mode (batch <= 64): the k-th group of units takes
+        // the sequence with the k-th longest context (ties by index), so the
+        // longest sequences start first and the short ones fill the CUs that
+        // free up (longest-processing-time-first list scheduling).  Lane s
+        // holds a key unique to sequence s; its rank is the number of larger
+        // keys.  Equal lengths keep the identity order without the count.
+        const int n = a.lpt_batch;
+        const int key = lane < n ? (seq_tokens(a.lens[lane], a.capacity) << 6) | (63 - lane) : -1;
+        const int len0 = __builtin_amdgcn_readlane(key, 0) >> 6;
+        if (__ballot(lane < n && (key >> 6) != len0) != 0) {
+            int g0 = 0, g1 = 0, g2 = 0, g3 = 0;
+            int t = 0;
+            for (; t + 4 <= n; t += 4) {
+                g0 += __builtin_amdgcn_readlane(key, t) > key ? 1 : 0;
+                g1 += __builtin_amdgcn_readlane(key, t + 1) > key ? 1 : 0;
+                g2 += __builtin_amdgcn_readlane(key, t + 2) > key ? 1 : 0;
+                g3 += __builtin_amdgcn_readlane(key, t + 3) > key ? 1 : 0;
+            }
+            for (; t < n; ++t) g0 += __builtin_amdgcn_readlane(key, t) > key ? 1 : 0;
+            b = __builtin_ctzll(__ballot(lane < n && g0 + g1 + g2 + g3 == b));
+        }
+        len = __builtin_amdgcn_readlane(key, b) >> 6;
+    } else {
+        len = seq_tokens(a.lens[b], a.capacity);
+    }
     const int kvh = r / a.gtiles;
     const int h0 = kvh * a.group + (r - kvh * a.gtiles) * G;
 
-    const int len = seq_tokens(a.lens[b], a.capacity);
     const int nparts = len > 0 ? (len + a.partition - 1) / a.partition : 1;
     if (part >= nparts) return;
     const int start = part * a.partition;
@@ -490,6 +517,7 @@ extern "C" int mvme_paged_attention(void* out, const void* query, const void* ke
     a.capacity = (int)(table_width * block_size);
     a.partition = p.partition;
     a.max_parts = p.max_parts;
+    a.lpt_batch = p.max_parts == 1 && batch >= 2 && batch <= kWave ? (int)batch : 0;
     a.scale_log2 = kLog2e / sqrtf((float)head_dim);
     const bool page_uniform = block_size % decode_tile_tokens(head_dim) == 0;
     hipStream_t s = static_cast<hipStream_t>(stream);

@@ -57,6 +57,31 @@ def test_hip_block_and_partition_boundaries(block_size, lengths, heads, kv_heads
     assert max_err(actual, oracle(args)) <= GATE[torch.bfloat16]
 
 
+@pytest.mark.parametrize("batch", [2, 37, 64])
+def test_longest_first_unit_order_keeps_each_sequence_its_own_output(batch):
+    """Whole-sequence mode hands units out longest context first; every
+    sequence must still get its own result, with ties, a one-token context
+    and lengths that change between calls on the same tables."""
+    gen = torch.Generator().manual_seed(900 + batch)
+    lengths = torch.randint(1, 700, (batch,), generator=gen)
+    lengths[: batch // 3] = 333  # ties keep the index order
+    lengths[-1] = 1
+    args = decode_inputs(torch.float16, lengths=tuple(lengths.tolist()), block_size=16, seed=batch)
+    dev = to_dev(args)
+    actual = paged_attention(*dev, backend="hip")
+    expected = oracle(args)
+    assert max_err(actual, expected) <= GATE[torch.float16]
+    for b in (0, batch // 2, batch - 1):  # each sequence alone gives the same rows
+        alone = paged_attention(dev[0][b:b + 1], dev[1], dev[2], dev[3][b:b + 1], dev[4][b:b + 1], 16,
+                                backend="hip")
+        assert (alone.float() - actual[b:b + 1].float()).abs().max().item() <= 2e-3
+    reversed_lens = dev[4].flip(0).contiguous()  # a permutation of the same lengths
+    args2 = list(args)
+    args2[4] = reversed_lens.cpu()
+    again = paged_attention(dev[0], dev[1], dev[2], dev[3], reversed_lens, 16, backend="hip")
+    assert max_err(again, oracle(args2)) <= GATE[torch.float16]
+
+
 @pytest.mark.parametrize("partition", [64, 128, 256, 512, 4096])
 def test_split_count_does_not_change_result(partition):
     """Split-K invariant: any partition size gives the single-partition answer."""
