@@ -382,7 +382,7 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     int64_t part;
     if (requested <= 0 && (units >= kDeviceCUs - kDeviceCUs / 16 || cap * units <= 64 * 1024)) {
         // Whole-sequence work-groups (also the launch-bound tiny case).
-        p.waves = cap >= 4 * whole_step ? kWholeWaves : kSplitWaves;
+        p.waves = cap >= 2 * whole_step ? kWholeWaves : kSplitWaves;
         part = (cap + tile - 1) / tile * tile;
     } else {
         p.waves = kSplitWaves;
