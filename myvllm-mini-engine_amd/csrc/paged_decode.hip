@@ -28,6 +28,8 @@ namespace {
 
 constexpr int kSplitWaves = 4;   // waves per work-group in split-K mode
 constexpr int kWholeWaves = 16;  // waves per work-group covering a whole sequence
+constexpr int kLptMax = 256;     // largest batch whose units go longest context first
+static_assert(kSplitWaves * kWave >= kLptMax, "one thread per sequence key");
 constexpr int kDecodeLoads = 4;  // K (and V) loads per lane per iteration
 
 template <int D>
@@ -59,7 +61,7 @@ struct DecodeArgs {
     int capacity;   // table_width * block_size
     int partition;  // tokens per partition (multiple of the wave tile)
     int max_parts;
-    int lpt_batch;  // batch size when units go longest sequence first (<= 64), else 0
+    int lpt_batch;  // batch size when units go longest sequence first (<= kLptMax), else 0
     float scale_log2;
 };
 
@@ -86,7 +88,31 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     int b = unit / per_seq;
     const int r = unit - b * per_seq;
     int len;
-    if (a.lpt_batch > 0) {
+    if (a.lpt_batch > kWave) {
+        // As below for 64 < batch <= kLptMax: thread s keeps sequence s's key
+        // in LDS and counts the larger keys with broadcast reads.
+        __shared__ int lpt_keys[kLptMax];
+        __shared__ int lpt_pick;
+        const int n = a.lpt_batch;
+        const int tid = threadIdx.x;
+        const int key = tid < n ? (seq_tokens(a.lens[tid], a.capacity) << 8) | (kLptMax - 1 - tid) : -1;
+        if (tid < ((n + 3) & ~3)) lpt_keys[tid] = key;  // -1 pads the last group of four
+        __syncthreads();
+        if (tid < n) {
+            int g0 = 0, g1 = 0, g2 = 0, g3 = 0;
+            for (int t = 0; t < n; t += 4) {
+                const int4 kv = *reinterpret_cast<const int4*>(&lpt_keys[t]);
+                g0 += kv.x > key ? 1 : 0;
+                g1 += kv.y > key ? 1 : 0;
+                g2 += kv.z > key ? 1 : 0;
+                g3 += kv.w > key ? 1 : 0;
+            }
+            if (g0 + g1 + g2 + g3 == b) lpt_pick = tid;
+        }
+        __syncthreads();
+        b = __builtin_amdgcn_readfirstlane(lpt_pick);
+        len = lpt_keys[b] >> 8;
+    } else if (a.lpt_batch > 0) {
         // Whole-sequence mode (batch <= 64): the k-th group of units takes
         // the sequence with the k-th longest context (ties by index), so the
         // longest sequences start first and the short ones fill the CUs that
@@ -517,7 +543,7 @@ extern "C" int mvme_paged_attention(void* out, const void* query, const void* ke
     a.capacity = (int)(table_width * block_size);
     a.partition = p.partition;
     a.max_parts = p.max_parts;
-    a.lpt_batch = p.max_parts == 1 && batch >= 2 && batch <= kWave ? (int)batch : 0;
+    a.lpt_batch = p.max_parts == 1 && batch >= 2 && batch <= kLptMax ? (int)batch : 0;
     a.scale_log2 = kLog2e / sqrtf((float)head_dim);
     const bool page_uniform = block_size % decode_tile_tokens(head_dim) == 0;
     hipStream_t s = static_cast<hipStream_t>(stream);

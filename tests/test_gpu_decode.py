@@ -57,7 +57,7 @@ def test_hip_block_and_partition_boundaries(block_size, lengths, heads, kv_heads
     assert max_err(actual, oracle(args)) <= GATE[torch.bfloat16]
 
 
-@pytest.mark.parametrize("batch", [2, 37, 64])
+@pytest.mark.parametrize("batch", [2, 37, 64, 65, 203, 256])
 def test_longest_first_unit_order_keeps_each_sequence_its_own_output(batch):
     """Whole-sequence mode hands units out longest context first; every
     sequence must still get its own result, with ties, a one-token context
