@@ -14,8 +14,14 @@ q, out, tables and lengths: 268,699,904 B per layer.
 
 Also reported (field "extra"): the other workloads of the same path --
 B=1/ctx128, B=8/ctx512 with the KV scatter, ragged B=64 with a shared
-prefix, and chunked prefill 8x128 on MFMA -- and the CPU torch path of the
-reference (restated in the oracle) timed on this host on a bounded sample.
+prefix, and chunked prefill 8x128 on MFMA.
+
+The CPU leg (field "cpu_baseline", off with --no-cpu-baseline) is the only
+part that touches the oracle: it times the reference's torch path (restated
+in the oracle) on this host on bounded samples -- one headline decode
+layer, and the chunked-prefill workload's KV scatter and prefill attention
+-- and, as the checker, computes the reference outputs that every GPU
+result above is compared with (the error fields are null without it).
 
 Prints ONE JSON line.
 """
@@ -45,6 +51,7 @@ LAYERS = 28
 BATCH, CONTEXT, BLOCK = 32, 2048, 256
 HQ, HKV, D = 16, 8, 128
 BASE_SEED = 20261026
+DECODE_NAMES = ("query", "key_cache", "value_cache", "block_tables", "context_lens")
 REFERENCE_US_PER_CALL = 362.44  # RTX 5080, block 256 fp16, decode_numerical_round_20261102.json:1693
 
 
@@ -115,19 +122,18 @@ def headline(args, torch, paged_attention, workloads):
     return layers, ms, eager_ms
 
 
-def headline_parity(layers, oracle):
-    """Layer 0 and layer 27 against the fp32 oracle (fp16 gate 2e-3)."""
+def headline_parity(layers, cpu):
+    """Layer 0 and layer 27 against the fp32 reference (fp16 gate 2e-3)."""
     worst = 0.0
     for idx in (0, LAYERS - 1):
         c = layers[idx]
         tensors = {"query": c["query"].cpu(), "key_cache": c["key_cache"].cpu(), "value_cache": c["value_cache"].cpu(),
                    "block_tables": c["block_tables"].cpu(), "context_lens": c["context_lens"].cpu()}
-        ref = oracle.fp32_oracle(tensors, BLOCK)
-        worst = max(worst, max_abs(c["out"], ref))
+        worst = max(worst, max_abs(c["out"], cpu.decode(tensors, BLOCK)))
     return {"layers_checked": [0, LAYERS - 1], "max_abs_error": worst, "gate": 2e-3, "passed": worst <= 2e-3}
 
 
-def decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_attention, oracle):
+def decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_attention, cpu):
     """The decode step as the engine runs it per layer (native_qwen3.py:179-197):
     write the batch's new K/V row at position len-1 of every sequence
     (write_kv_cache_batch), then paged attention over the updated context --
@@ -153,17 +159,20 @@ def decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_at
     rows_k = c["key_cache"].cpu()[pages, offsets % BLOCK]
     rows_v = c["value_cache"].cpu()[pages, offsets % BLOCK]
     scatter_ok = torch.equal(rows_k, c["new_key"].cpu()) and torch.equal(rows_v, c["new_value"].cpu())
-    tensors = {"query": c["query"].cpu(), "key_cache": c["key_cache"].cpu(), "value_cache": c["value_cache"].cpu(),
-               "block_tables": tables, "context_lens": c["context_lens"].cpu()}
-    err = max_abs(c["out"], oracle.fp32_oracle(tensors, BLOCK))
+    err = None
+    if cpu is not None:
+        tensors = {"query": c["query"].cpu(), "key_cache": c["key_cache"].cpu(),
+                   "value_cache": c["value_cache"].cpu(), "block_tables": tables,
+                   "context_lens": c["context_lens"].cpu()}
+        err = max_abs(c["out"], cpu.decode(tensors, BLOCK))
     step_bytes = LAYERS * (layer_bytes() + 2 * BATCH * HKV * D * 2 * 2 + BATCH * 8)
     return {"us_per_step": ms * 1e3, "us_per_layer": ms * 1e3 / LAYERS,
             "TBps": step_bytes / (ms * 1e-3) / 1e12, "launches_per_step": 2 * LAYERS,
             "scatter_bit_exact": scatter_ok, "max_abs_error_layer0": err, "gate": 2e-3,
-            "passed": scatter_ok and err <= 2e-3}
+            "passed": scatter_ok and (err is None or err <= 2e-3)}
 
 
-def decode_attention_block_step(args, torch, layers, paged_attention, oracle):
+def decode_attention_block_step(args, torch, layers, paged_attention, cpu):
     """The attention block of the decode step for all 28 headline layers in one captured graph:
     per layer the fused q/k RMSNorm + RoPE + KV page write of the new token (replacing q_norm,
     k_norm, apply_rope and write_kv_cache_batch, native_qwen3.py:179-191), paged attention over
@@ -201,21 +210,23 @@ def decode_attention_block_step(args, torch, layers, paged_attention, oracle):
             torch.mm(c["out"].view(BATCH, HQ * D), c["w_o"], out=c["hidden"])
 
     ms, _ = graph_time_ms(step, torch, calls_per_graph=3 * LAYERS, replays=args.steps, warmup=args.warmup)
-    # Layer 0 against the oracle: the rotated q, the written K/V rows, attention, o_proj.
+    # Layer 0 against the reference: the rotated q, the written K/V rows, attention, o_proj.
     c = layers[0]
-    q, k, v = (t.cpu() for t in split(c))
-    tables, positions = c["block_tables"].cpu(), c["positions"].cpu()
-    kc, vc = c["key_cache"].cpu(), c["value_cache"].cpu()
-    kc_o, vc_o = kc.clone(), vc.clone()
-    q_ref = oracle.qk_norm_rope_write_kv(q, k, v, c["wq"].cpu(), c["wk"].cpu(), c["cos"].cpu(), c["sin"].cpu(),
-                                         kc_o, vc_o, block_tables=tables, positions=positions)
-    rope_err = max(max_abs(c["q_rot"], q_ref), max_abs(kc, kc_o))
-    v_exact = torch.equal(vc, vc_o)
-    tensors = {"query": c["q_rot"].cpu(), "key_cache": kc, "value_cache": vc, "block_tables": tables,
-               "context_lens": c["context_lens"].cpu()}
-    attn_err = max_abs(c["out"], oracle.fp32_oracle(tensors, BLOCK))
-    o_err = max_abs(c["hidden"], c["out"].float().cpu().view(BATCH, -1) @ c["w_o"].float().cpu())
-    passed = v_exact and rope_err <= 4e-3 and attn_err <= 2e-3 and o_err <= 2e-2
+    v_exact = rope_err = attn_err = o_err = passed = None
+    if cpu is not None:
+        q, k, v = (t.cpu() for t in split(c))
+        tables, positions = c["block_tables"].cpu(), c["positions"].cpu()
+        kc, vc = c["key_cache"].cpu(), c["value_cache"].cpu()
+        kc_o, vc_o = kc.clone(), vc.clone()
+        q_ref = cpu.norm_rope_write_kv(q, k, v, c["wq"].cpu(), c["wk"].cpu(), c["cos"].cpu(), c["sin"].cpu(),
+                                       kc_o, vc_o, block_tables=tables, positions=positions)
+        rope_err = max(max_abs(c["q_rot"], q_ref), max_abs(kc, kc_o))
+        v_exact = torch.equal(vc, vc_o)
+        tensors = {"query": c["q_rot"].cpu(), "key_cache": kc, "value_cache": vc, "block_tables": tables,
+                   "context_lens": c["context_lens"].cpu()}
+        attn_err = max_abs(c["out"], cpu.decode(tensors, BLOCK))
+        o_err = max_abs(c["hidden"], c["out"].float().cpu().view(BATCH, -1) @ c["w_o"].float().cpu())
+        passed = v_exact and rope_err <= 4e-3 and attn_err <= 2e-3 and o_err <= 2e-2
     for c in layers:
         for key in ("qkv", "wq", "wk", "cos", "sin", "w_o", "positions", "q_rot", "hidden"):
             del c[key]
@@ -224,36 +235,99 @@ def decode_attention_block_step(args, torch, layers, paged_attention, oracle):
             "max_abs_error_attention_layer0": attn_err, "max_abs_error_o_proj_layer0": o_err, "passed": passed}
 
 
-def cpu_baseline(layers, oracle, torch, budget_s):
-    """The reference's torch decode path, restated in the oracle, on host cores."""
-    threads = torch.get_num_threads()
-    c = layers[0]
-    tensors = [c["query"].cpu(), c["key_cache"].cpu(), c["value_cache"].cpu(), c["block_tables"].cpu(),
-               c["context_lens"].cpu()]
-    oracle.paged_attention(*tensors, BLOCK)  # warm-up
+def _median_seconds(fn, budget_s, min_runs=5, max_runs=20):
+    """Median wall time of fn() after one warm-up: at least min_runs runs, more
+    while inside the budget (never past 3x the budget)."""
+    fn()
     samples = []
     t_start = time.perf_counter()
-    while len(samples) < 5 or (time.perf_counter() - t_start < budget_s and len(samples) < 20):
+    while len(samples) < min_runs or (time.perf_counter() - t_start < budget_s and len(samples) < max_runs):
         t0 = time.perf_counter()
-        oracle.paged_attention(*tensors, BLOCK)
+        fn()
         samples.append(time.perf_counter() - t0)
         if time.perf_counter() - t_start > 3 * budget_s:
             break
-    sec = statistics.median(samples)
-    cpu_model = platform.processor() or ""
-    try:
-        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
-        for line in out.splitlines():
-            if line.startswith("Model name:"):
-                cpu_model = line.split(":", 1)[1].strip()
-    except Exception:
-        pass
-    return {"value": layer_bytes() / sec / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
-            "us_per_call": sec * 1e6,
-            "sample": (f"one layer of the headline step (B=32, ctx 2048, fp16, block 256) through the "
-                       f"reference's torch decode path (fallback.py:27-64, restated in oracle/paged_oracle.py); "
-                       f"median of {len(samples)} runs after 1 warm-up; torch threads={threads}, "
-                       f"os.cpu_count()={os.cpu_count()}, cpu={cpu_model}")}
+    return statistics.median(samples), len(samples)
+
+
+class CpuLeg:
+    """The CPU leg: the reference's torch path restated in the oracle, on the
+    host cores.  It is the only user of the oracle in this file -- as the
+    timed CPU baseline and as the checker that computes the reference outputs
+    the GPU results are compared with."""
+
+    def __init__(self, torch):
+        from oracle import paged_oracle
+
+        self.torch = torch
+        self.oracle = paged_oracle
+
+    # Reference outputs (the checker).
+    def decode(self, tensors, block_size):
+        return self.oracle.fp32_oracle(tensors, block_size)
+
+    def prefill(self, *args, **kwargs):
+        return self.oracle.paged_prefill_attention(*args, **kwargs)
+
+    def norm_rope_write_kv(self, *args, **kwargs):
+        return self.oracle.qk_norm_rope_write_kv(*args, **kwargs)
+
+    def greedy(self, logits):
+        return self.oracle.greedy_argmax(logits)
+
+    # Timed baselines.
+    def cpu_model(self):
+        model = platform.processor() or ""
+        try:
+            out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+            for line in out.splitlines():
+                if line.startswith("Model name:"):
+                    model = line.split(":", 1)[1].strip()
+        except Exception:
+            pass
+        return model
+
+    def baseline(self, workloads, budget_s):
+        """Headline fields (one decode layer), plus the chunked-prefill workload's
+        scatter and prefill attention under "other_workloads"."""
+        torch = self.torch
+        threads = torch.get_num_threads()
+        c = workloads.decode_b32_layer(torch.device("cuda:0"), seed=BASE_SEED + 2)
+        tensors = [c["query"].cpu(), c["key_cache"].cpu(), c["value_cache"].cpu(), c["block_tables"].cpu(),
+                   c["context_lens"].cpu()]
+        del c
+        sec, runs = _median_seconds(lambda: self.oracle.paged_attention(*tensors, BLOCK), budget_s)
+        del tensors
+        cpu_model = self.cpu_model()
+        result = {"value": layer_bytes() / sec / 1e12, "unit": "TB/s", "cores": threads, "kind": "port",
+                  "us_per_call": sec * 1e6,
+                  "sample": (f"one layer of the headline step (B=32, ctx 2048, fp16, block 256) through the "
+                             f"reference's torch decode path (fallback.py:27-64, restated in oracle/paged_oracle.py); "
+                             f"median of {runs} runs after 1 warm-up; torch threads={threads}, "
+                             f"os.cpu_count()={os.cpu_count()}, cpu={cpu_model}")}
+        # Chunked prefill 8 x 128 (bf16, block 256): the reference's torch scatter
+        # (index_copy_, data.py:120-125) and torch prefill (prefill.py:114-131).
+        pc = workloads.chunked_prefill_case(device=torch.device("cuda:0"))
+        cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in pc.items()}
+        del pc
+        kc, vc = cpu["key_cache"].clone(), cpu["value_cache"].clone()
+        scatter = lambda: self.oracle.write_kv_cache_slots(kc, vc, cpu["slot_mapping"], cpu["new_key"],  # noqa: E731
+                                                           cpu["new_value"])
+        s_sec, s_runs = _median_seconds(scatter, budget_s / 4)
+        names = ("q", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+        q, cu, st, tb, ln = (cpu[n] for n in names)
+        prefill = lambda: self.oracle.paged_prefill_attention(q, kc, vc, cu, st, tb, ln, 256)  # noqa: E731
+        p_sec, p_runs = _median_seconds(prefill, budget_s / 2)
+        flops = workloads.prefill_flops(cpu["priors"])
+        moved = 2 * 1024 * HKV * D * 2 * 2 + 1024 * 8
+        result["other_workloads"] = {
+            "kv_scatter_1024_tokens_bf16": {
+                "us_per_call": s_sec * 1e6, "GBps": moved / s_sec / 1e9,
+                "sample": f"the 1024 new K/V rows of the chunked-prefill workload, median of {s_runs} runs"},
+            "chunked_prefill_8x128_bf16": {
+                "us_per_call": p_sec * 1e6, "TFLOPs": flops / p_sec / 1e12,
+                "sample": f"8 sequences x 128 new tokens, priors {cpu['priors']}, median of {p_runs} runs"}}
+        return result
 
 
 # ---------------------------------------------------------------------------
@@ -263,26 +337,26 @@ def cpu_baseline(layers, oracle, torch, budget_s):
 EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "norm_rope", "after_attention")
 
 
-def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, oracle,
+def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, cpu,
                     names=EXTRA_NAMES):
     dev = torch.device("cuda:0")
     extra = {}
     if "decode_b1" in names:
-        _extra_b1(torch, paged_attention, workloads, oracle, dev, extra)
+        _extra_b1(torch, paged_attention, workloads, cpu, dev, extra)
     if "decode_b8" in names:
-        _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, oracle, dev, extra)
+        _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, cpu, dev, extra)
     if "ragged_b64" in names:
-        _extra_ragged(torch, paged_attention, workloads, oracle, dev, extra)
+        _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra)
     if "prefill" in names:
-        _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, oracle, dev, extra)
+        _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra)
     if "norm_rope" in names:
-        _extra_norm_rope(torch, oracle, dev, extra)
+        _extra_norm_rope(torch, cpu, dev, extra)
     if "after_attention" in names:
-        _extra_after_attention(torch, oracle, dev, extra)
+        _extra_after_attention(torch, cpu, dev, extra)
     return extra
 
 
-def _extra_b1(torch, paged_attention, workloads, oracle, dev, extra):
+def _extra_b1(torch, paged_attention, workloads, cpu, dev, extra):
     # B=1 / ctx 128, fp16, block 256.
     c = workloads.decode_b1(dev)
     out = torch.empty_like(c["query"])
@@ -295,13 +369,13 @@ def _extra_b1(torch, paged_attention, workloads, oracle, dev, extra):
                 fn()
         return run
     ms, _ = graph_time_ms(many(), torch, calls_per_graph=50, replays=20, warmup=3)
-    ref = oracle.fp32_oracle({k: c[k].cpu() for k in oracle.TENSOR_NAMES}, 256)
+    err = None if cpu is None else max_abs(out, cpu.decode({k: c[k].cpu() for k in DECODE_NAMES}, 256))
     bytes_b1 = 1 * 128 * 4096 + 2 * 16 * 128 * 2 + 8 + 8
     extra["decode_b1_ctx128_fp16"] = {"us_per_call": ms / 50 * 1e3, "GBps": bytes_b1 / (ms / 50 * 1e-3) / 1e9,
-                                      "max_abs_error": max_abs(out, ref), "reference_rtx5080_us": 18.945}
+                                      "max_abs_error": err, "reference_rtx5080_us": 18.945}
 
 
-def _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, oracle, dev, extra):
+def _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, cpu, dev, extra):
     # B=8 / ctx 512, bf16, block 16, + scatter of the new token.
     c = workloads.decode_b8_with_scatter(dev)
     out = torch.empty_like(c["query"])
@@ -320,15 +394,18 @@ def _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, oracle, d
     ms, _ = graph_time_ms(many2(), torch, calls_per_graph=50, replays=20, warmup=3)
     kc, vc = c["key_cache"].cpu(), c["value_cache"].cpu()
     slots_ok = torch.equal(kc.view(-1, 8, 128)[c["slot_mapping"].cpu()], c["new_key"].cpu())
-    ref = oracle.fp32_oracle({"query": c["query"].cpu(), "key_cache": kc, "value_cache": vc,
-                              "block_tables": c["block_tables"].cpu(), "context_lens": c["context_lens"].cpu()}, 16)
+    err = None
+    if cpu is not None:
+        err = max_abs(out, cpu.decode({"query": c["query"].cpu(), "key_cache": kc, "value_cache": vc,
+                                       "block_tables": c["block_tables"].cpu(),
+                                       "context_lens": c["context_lens"].cpu()}, 16))
     bytes_b8 = 8 * 512 * 4096 + 2 * 8 * 16 * 128 * 2 + 8 * 32 * 8 + 8 * 8
     extra["decode_b8_ctx512_bf16_with_scatter"] = {
         "us_per_call": ms / 50 * 1e3, "GBps_decode_bytes": bytes_b8 / (ms / 50 * 1e-3) / 1e9,
-        "scatter_bit_exact": bool(slots_ok), "max_abs_error": max_abs(out, ref), "reference_rtx5080_us": 40.340}
+        "scatter_bit_exact": bool(slots_ok), "max_abs_error": err, "reference_rtx5080_us": 40.340}
 
 
-def _extra_ragged(torch, paged_attention, workloads, oracle, dev, extra):
+def _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra):
     # Ragged B=64, ctx U[1,4096], bf16, block 16, shared 1024-token prefix.
     c = workloads.ragged_shared_prefix_case(device=dev)
     out = torch.empty_like(c["query"])
@@ -344,15 +421,15 @@ def _extra_ragged(torch, paged_attention, workloads, oracle, dev, extra):
     per_call = ms / 10 * 1e-3
     unique = c["unique_rows"] * 4096 + 2 * 64 * 16 * 128 * 2 + 64 * 256 * 8 + 64 * 8
     logical = c["logical_rows"] * 4096 + 2 * 64 * 16 * 128 * 2 + 64 * 256 * 8 + 64 * 8
-    ref = oracle.fp32_oracle({k: c[k].cpu() for k in oracle.TENSOR_NAMES}, 16)
+    err = None if cpu is None else max_abs(out, cpu.decode({k: c[k].cpu() for k in DECODE_NAMES}, 16))
     extra["ragged_b64_shared_prefix_bf16"] = {
         "us_per_call": per_call * 1e6, "GBps_unique": unique / per_call / 1e9,
         "frac_of_hbm_peak_unique": unique / per_call / 1e9 / HBM_PEAK_GBS,
         "GBps_logical": logical / per_call / 1e9, "unique_rows": c["unique_rows"], "logical_rows": c["logical_rows"],
-        "max_abs_error": max_abs(out, ref)}
+        "max_abs_error": err}
 
 
-def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, oracle, dev, extra):
+def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra):
     # Chunked prefill: 8 x 128 new tokens after U[0,3968] prior, bf16, block 256.
     c = workloads.chunked_prefill_case(device=dev)
     names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
@@ -373,12 +450,12 @@ def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloa
     per_call = ms / 10 * 1e-3
     flops = workloads.prefill_flops(c["priors"])
     kv_bytes = sum(p + 128 for p in c["priors"]) * 4096 + 2 * 1024 * 16 * 128 * 2
-    ref = oracle.paged_prefill_attention(*[a.cpu() for a in pargs], 256, cast=False)
+    err = None if cpu is None else max_abs(holder["out"], cpu.prefill(*[a.cpu() for a in pargs], 256, cast=False))
     extra["chunked_prefill_8x128_bf16"] = {
         "us_per_call": per_call * 1e6, "TFLOPs": flops / per_call / 1e12,
         "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "GBps": kv_bytes / per_call / 1e9, "flops": flops, "priors": c["priors"],
-        "max_abs_error": max_abs(holder["out"], ref)}
+        "max_abs_error": err}
 
 
 def _norm_rope_case(torch, dev, tokens, dtype, seed):
@@ -394,7 +471,7 @@ def _norm_rope_case(torch, dev, tokens, dtype, seed):
     return c
 
 
-def _extra_norm_rope(torch, oracle, dev, extra):
+def _extra_norm_rope(torch, cpu_leg, dev, extra):
     """Fused q/k RMSNorm + RoPE + KV write at the prefill batch (1024 tokens, bf16, block 256, slot
     mapping) and the decode batch (32 sequences, fp16, block 256, tables + positions), beside the same
     four steps as separate eager torch ops plus the HIP scatter (the reference's torch data path, timed
@@ -450,27 +527,31 @@ def _extra_norm_rope(torch, oracle, dev, extra):
         per_call = ms / 50 * 1e-3
         moved = (tokens * (HQ + 2 * HKV) * D * 2 + tokens * D * 2 + 2 * D * 2 + tokens * 8 * (2 if mode == "tables"
                  else 1) + tokens * HQ * D * 2 + tokens * 2 * HKV * D * 2)
-        # Parity of the last call against the oracle (q rows; written K rows; V rows bit-exact).
-        fused()
-        torch.cuda.synchronize()
-        cpu = {k: v.cpu() for k, v in c.items()}
-        kc_o, vc_o = torch.zeros(pages, BLOCK, HKV, D, dtype=dtype), torch.zeros(pages, BLOCK, HKV, D, dtype=dtype)
-        cpu_meta = {k: v.cpu() for k, v in meta.items()}
-        want_q = oracle.qk_norm_rope_write_kv(cpu["q"], cpu["k"], cpu["v"], cpu["wq"], cpu["wk"], cpu["cos"],
-                                              cpu["sin"], kc_o, vc_o, **cpu_meta)
-        rows = slots.cpu()
-        got_k, want_k = kc.cpu().view(-1, HKV, D)[rows], kc_o.view(-1, HKV, D)[rows]
         extra[name] = {
             "us_per_call": per_call * 1e6, "GBps": moved / per_call / 1e9,
             "frac_of_hbm_peak": moved / per_call / 1e9 / HBM_PEAK_GBS, "algorithmic_bytes": moved,
             "eager_torch_four_steps_us": eager_ms / 10 * 1e3,
-            "q_max_abs_error": max_abs(out, want_q),
-            "q_bit_identical_frac": (out.cpu() == want_q).float().mean().item(),
-            "k_max_abs_error": max_abs(got_k, want_k),
-            "v_bit_exact": bool(torch.equal(vc.cpu().view(-1, HKV, D)[rows], vc_o.view(-1, HKV, D)[rows]))}
+            "q_max_abs_error": None, "q_bit_identical_frac": None, "k_max_abs_error": None, "v_bit_exact": None}
+        if cpu_leg is not None:
+            # The last call against the reference (q rows; written K rows; V rows bit-exact).
+            fused()
+            torch.cuda.synchronize()
+            cpu = {k: v.cpu() for k, v in c.items()}
+            kc_o = torch.zeros(pages, BLOCK, HKV, D, dtype=dtype)
+            vc_o = torch.zeros(pages, BLOCK, HKV, D, dtype=dtype)
+            cpu_meta = {k: v.cpu() for k, v in meta.items()}
+            want_q = cpu_leg.norm_rope_write_kv(cpu["q"], cpu["k"], cpu["v"], cpu["wq"], cpu["wk"], cpu["cos"],
+                                                cpu["sin"], kc_o, vc_o, **cpu_meta)
+            rows = slots.cpu()
+            got_k, want_k = kc.cpu().view(-1, HKV, D)[rows], kc_o.view(-1, HKV, D)[rows]
+            extra[name].update({
+                "q_max_abs_error": max_abs(out, want_q),
+                "q_bit_identical_frac": (out.cpu() == want_q).float().mean().item(),
+                "k_max_abs_error": max_abs(got_k, want_k),
+                "v_bit_exact": bool(torch.equal(vc.cpu().view(-1, HKV, D)[rows], vc_o.view(-1, HKV, D)[rows]))})
 
 
-def _extra_after_attention(torch, oracle, dev, extra):
+def _extra_after_attention(torch, cpu, dev, extra):
     """The step after attention at the headline batch: o_proj GEMV (a library GEMM, hipBLASLt
     through torch.mm, as the reference's CudaLinear uses cuBLAS) and greedy argmax over a
     151,936-entry vocabulary (the HIP kernel), 32 sequences, hidden 2048."""
@@ -503,7 +584,8 @@ def _extra_after_attention(torch, oracle, dev, extra):
         moved = batch * vocab * logits.element_size() + batch * 8
         extra[name] = {"us_per_call": ms / 50 * 1e3, "GBps": moved / (ms / 50 * 1e-3) / 1e9,
                        "frac_of_hbm_peak": moved / (ms / 50 * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                       "tokens_equal_oracle": bool(torch.equal(tokens.cpu(), oracle.greedy_argmax(logits.cpu())))}
+                       "tokens_equal_reference": None if cpu is None else
+                       bool(torch.equal(tokens.cpu(), cpu.greedy(logits.cpu())))}
 
 
 def main(argv=None):
@@ -534,7 +616,6 @@ def main(argv=None):
     from mini_engine_hip.kernels.paged import paged_attention
     from mini_engine_hip.kernels.prefill import paged_prefill_attention
     from mini_engine_hip import workloads
-    from oracle import paged_oracle
 
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
@@ -549,9 +630,11 @@ def main(argv=None):
         return 0
     lib = hip_extension.load_hip_extension()
     log(f"library {lib.path}")
+    # The CPU leg (timed reference path and checker); nothing else uses the oracle.
+    cpu = None if args.no_cpu_baseline else CpuLeg(torch)
     if args.no_headline:
         extra = extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads,
-                                paged_oracle, names=tuple(args.extra.split(",")))
+                                cpu, names=tuple(args.extra.split(",")))
         print(json.dumps({"profiling_run": True, "extra": extra}), flush=True)
         return 0
 
@@ -560,14 +643,13 @@ def main(argv=None):
     step_bytes = LAYERS * layer_bytes()
     achieved_gbs = layer_bytes() / (per_call_ms * 1e-3) / 1e9
     log(f"headline: {step_ms:.3f} ms/step, {per_call_ms * 1e3:.2f} us/call, {achieved_gbs:.0f} GB/s")
-    parity = headline_parity(layers, paged_oracle)
+    parity = None if cpu is None else headline_parity(layers, cpu)
     log(f"parity: {parity}")
     decode_step = attention_block = None
     if not args.no_extra:
-        decode_step = decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_attention,
-                                               paged_oracle)
+        decode_step = decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_attention, cpu)
         log(f"decode step with scatter: {decode_step}")
-        attention_block = decode_attention_block_step(args, torch, layers, paged_attention, paged_oracle)
+        attention_block = decode_attention_block_step(args, torch, layers, paged_attention, cpu)
         log(f"decode attention block: {attention_block}")
 
     traffic = None
@@ -607,13 +689,12 @@ def main(argv=None):
     torch.cuda.empty_cache()
     if not args.no_extra:
         result["extra"] = extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention,
-                                          workloads, paged_oracle, names=tuple(args.extra.split(",")))
+                                          workloads, cpu, names=tuple(args.extra.split(",")))
         result["extra"]["decode_step_b32_ctx2048_28layers_with_scatter"] = decode_step
         result["extra"]["decode_attention_block_b32_ctx2048_28layers"] = attention_block
         log(f"extra: {json.dumps(result['extra'])}")
-    if not args.no_cpu_baseline:
-        gen_layers = [workloads.decode_b32_layer(torch.device("cuda:0"), seed=BASE_SEED + 2)]
-        result["cpu_baseline"] = cpu_baseline(gen_layers, paged_oracle, torch, args.cpu_budget)
+    if cpu is not None:
+        result["cpu_baseline"] = cpu.baseline(workloads, args.cpu_budget)
         log(f"cpu baseline: {result['cpu_baseline']}")
     print(json.dumps(result), flush=True)
     return 0
