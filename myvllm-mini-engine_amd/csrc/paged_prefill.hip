@@ -212,14 +212,6 @@ __device__ inline void lds_dma16(const void* gptr, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(gptr), "s"(base) : "m0");
 }
 
-// Wave-wide waits + work-group barrier with a compiler memory fence.
-__device__ inline void dma_landed_barrier() {
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
-}
-__device__ inline void lds_reads_done_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory");
-}
-
 template <typename P>
 __device__ inline uint32_t lds_addr(P* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)p;
@@ -234,6 +226,18 @@ constexpr float kPSumLimit = 256.f;
 // Full wait issued through the builtin, which the compiler's own wait
 // insertion understands (it then knows earlier loads have completed).
 __device__ inline void wait_vmcnt_all() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Every load and LDS access of this wave complete, then the work-group
+// barrier (with a compiler memory fence).  The wait goes through the builtin
+// so that the compiler knows the Q operand loads have landed too: written in
+// the barrier's inline assembly instead, it is invisible to the compiler,
+// which then adds its own vmcnt(0) before the first use of Q in every tile --
+// and that wait also covers the copies issued right after the barrier, so
+// every pair of tiles waited for the next pair's copies to land.
+__device__ inline void landed_barrier() {
+    wait_vmcnt_all();
+    asm volatile("s_barrier" : : : "memory");
+}
 
 // Max / sum over the four lanes {l, l^16, l^32, l^48} (the 4 MFMA k-groups
 // holding one query row) with gfx950 lane swaps -- no LDS round trip.
@@ -515,7 +519,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         // Both tiles of the pair have landed (this lane's copies, then every
         // lane's through the barrier), and every wave is done with the
         // previous pair, whose stages the copies below refill.
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" : : : "memory");
+        landed_barrier();
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             lookup(tp + 2 + k);
