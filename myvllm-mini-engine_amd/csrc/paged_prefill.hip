@@ -783,23 +783,31 @@ __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(Pref
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         for (int c0 = 0; c0 < nchunks; c0 += kGroup) {
             using P = typename PartialOf<T>::type;
-            f32x4 x[kGroup][2];
+            // Every load of the group is issued before any is used (loads
+            // guarded one by one, each followed by its use, would each wait
+            // for the previous one).  Chunks past the last re-read the last
+            // one -- in bounds and cached -- and get weight zero below.
+            u32x4 raw[kGroup][2];
             float2 mlc[kGroup];
 #pragma unroll
             for (int k = 0; k < kGroup; ++k) {
-                x[k][0] = x[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-                mlc[k] = float2{kNegInf, 0.f};
-                if (c0 + k < nchunks) {
-                    const P* po = static_cast<const P*>(a.ws_o) + (slot0 + c0 + k) * kPfD + d0;
-                    if constexpr (sizeof(P) == 4) {
-                        x[k][0] = reinterpret_cast<const f32x4*>(po)[0];
-                        x[k][1] = reinterpret_cast<const f32x4*>(po)[1];
-                    } else {
-                        const u32x4 w = *reinterpret_cast<const u32x4*>(po);
-                        x[k][0] = f32x4{T::lo(w[0]), T::hi(w[0]), T::lo(w[1]), T::hi(w[1])};
-                        x[k][1] = f32x4{T::lo(w[2]), T::hi(w[2]), T::lo(w[3]), T::hi(w[3])};
-                    }
-                    mlc[k] = ml[c0 + k];
+                const int c = min(c0 + k, nchunks - 1);
+                const u32x4* po = reinterpret_cast<const u32x4*>(static_cast<const P*>(a.ws_o) + (slot0 + c) * kPfD + d0);
+                raw[k][0] = po[0];
+                if constexpr (sizeof(P) == 4) raw[k][1] = po[1];
+                mlc[k] = ml[c];
+            }
+            f32x4 x[kGroup][2];
+#pragma unroll
+            for (int k = 0; k < kGroup; ++k) {
+                if (c0 + k >= nchunks) mlc[k] = float2{kNegInf, 0.f};
+                if constexpr (sizeof(P) == 4) {
+                    x[k][0] = __builtin_bit_cast(f32x4, raw[k][0]);
+                    x[k][1] = __builtin_bit_cast(f32x4, raw[k][1]);
+                } else {
+                    const u32x4 w = raw[k][0];
+                    x[k][0] = f32x4{T::lo(w[0]), T::hi(w[0]), T::lo(w[1]), T::hi(w[1])};
+                    x[k][1] = f32x4{T::lo(w[2]), T::hi(w[2]), T::lo(w[3]), T::hi(w[3])};
                 }
             }
             float gmax = kNegInf;
