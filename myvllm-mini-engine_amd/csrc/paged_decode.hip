@@ -345,8 +345,17 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
 // Split-K combine: out = sum_p acc_p 2^(m_p - M) / sum_p l_p 2^(m_p - M).
 // Partitions that never saw a valid token carry m = -inf and contribute 0;
 // an all-empty sequence produces 0.
+// One work-group of D threads per (sequence, query head); thread t owns
+// output dim t.  Every step loads many partitions at once: the
+// partition maxima one per thread, then (per window of partitions) the
+// weights 2^(m_p - ref) into LDS and each dim's partials eight at a time.
+constexpr int kMergeWindow = 2048;  // partition weights held in LDS at once
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
+    static_assert(D <= 256, "one thread per output dim");
+    __shared__ float sm_red[256 / kWave];
+    __shared__ float sm_w[kMergeWindow];
     const int64_t bh = blockIdx.x;
     const int b = (int)(bh / a.q_heads);
     const int len = seq_tokens(a.lens[b], a.capacity);
@@ -354,16 +363,55 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
     if (nparts == 1) return;  // written directly by the attention kernel
     const float* ml = a.ws_ml + bh * a.max_parts * 2;
     const float* acc = a.ws_acc + bh * a.max_parts * D;
+    const int tid = threadIdx.x;
+    const int lane = tid & (kWave - 1), wave = tid / kWave;
+    constexpr int kWaves = (D + kWave - 1) / kWave;
+    auto block_reduce = [&](float v, bool is_max) __attribute__((always_inline)) {
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) {
+            const float o = __shfl_xor(v, off);
+            v = is_max ? fmaxf(v, o) : v + o;
+        }
+        __syncthreads();  // earlier reads of sm_red are done
+        if (lane == 0) sm_red[wave] = v;
+        __syncthreads();
+        v = sm_red[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) v = is_max ? fmaxf(v, sm_red[w]) : v + sm_red[w];
+        return v;
+    };
     float mx = kNegInf;
-    for (int p = 0; p < nparts; ++p) mx = fmaxf(mx, ml[2 * p]);
+    for (int p = tid; p < nparts; p += D) mx = fmaxf(mx, ml[2 * p]);
+    mx = block_reduce(mx, true);
     const float ref = mx == kNegInf ? 0.f : mx;
-    float sum = 0.f;
-    for (int p = 0; p < nparts; ++p) sum += ml[2 * p + 1] * fast_exp2(ml[2 * p] - ref);
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        float o = 0.f;
-        for (int p = 0; p < nparts; ++p) o += acc[(int64_t)p * D + d] * fast_exp2(ml[2 * p] - ref);
-        static_cast<uint16_t*>(a.out)[bh * D + d] = T::from_float(sum > 0.f ? o / sum : 0.f);
+    constexpr int kBatch = 8;
+    float o = 0.f, sum = 0.f;
+    for (int w0 = 0; w0 < nparts; w0 += kMergeWindow) {
+        const int n = min(kMergeWindow, nparts - w0);
+        __syncthreads();  // the previous window's weights are no longer read
+        for (int p = tid; p < n; p += D) {
+            const float w = fast_exp2(ml[2 * (w0 + p)] - ref);
+            sm_w[p] = w;
+            sum += ml[2 * (w0 + p) + 1] * w;
+        }
+        __syncthreads();
+        const float* accw = acc + (int64_t)w0 * D + tid;
+        for (int p0 = 0; p0 < n; p0 += kBatch) {
+            // Indices past the window's last partition re-read it; the
+            // select drops them.
+            float av[kBatch], wv[kBatch];
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int pk = min(p0 + k, n - 1);
+                av[k] = accw[(int64_t)pk * D];
+                wv[k] = sm_w[pk];
+            }
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) o += p0 + k < n ? av[k] * wv[k] : 0.f;
+        }
     }
+    sum = block_reduce(sum, false);
+    static_cast<uint16_t*>(a.out)[bh * D + tid] = T::from_float(sum > 0.f ? o / sum : 0.f);
 }
 
 struct DecodePlan {
@@ -390,10 +438,10 @@ int decode_tile_tokens(int64_t head_dim) {
 constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 
 // Host-side plan (lengths stay on the device, so it depends on the table
-// capacity only).  Enough (sequence, kv head) units to occupy every CU: one
-// 16-wave work-group per unit over the whole context, merged in LDS.
-// Fewer units: split-K into partitions of 4-wave work-groups, sized to give
-// every CU about four work-groups, plus a merge kernel.  `requested` > 0
+// capacity only).  Enough (sequence, kv head) units to occupy every CU, or a
+// short capacity: one work-group per unit over the whole context, merged in
+// LDS.  Otherwise split-K into partitions of 4-wave work-groups, sized to
+// give every CU about four work-groups, plus a merge kernel.  `requested` > 0
 // forces split-K with that partition length (rounded to the wave tiling).
 DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                             int64_t block_size, int64_t table_width, int64_t requested) {
@@ -406,8 +454,11 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     const int64_t split_step = tile * kSplitWaves;
     const int64_t whole_step = tile * kWholeWaves;
     int64_t part;
-    if (requested <= 0 && (units >= kDeviceCUs - kDeviceCUs / 16 || cap * units <= 64 * 1024)) {
-        // Whole-sequence work-groups (also the launch-bound tiny case).
+    if (requested <= 0 && (units >= kDeviceCUs - kDeviceCUs / 16 || cap <= 2 * whole_step)) {
+        // Whole-sequence work-groups; also when the capacity is at most two
+        // 16-wave steps (launch- and latency-bound, a merge would only add a
+        // launch).  Longer contexts with few units split instead, so that a
+        // few work-groups do not each walk a long context alone.
         p.waves = cap >= 2 * whole_step ? kWholeWaves : kSplitWaves;
         part = (cap + tile - 1) / tile * tile;
     } else {
@@ -443,7 +494,7 @@ void launch_decode(const DecodeArgs& a, int waves, int units, bool page_uniform,
     else launch_decode_nw<T, D, G, kSplitWaves>(a, units, page_uniform, s);
     if (a.max_parts > 1)
         hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(units / a.kv_heads / a.gtiles * a.q_heads),
-                           dim3(D < 256 ? D : 256), 0, s, a);
+                           dim3(D), 0, s, a);
 }
 
 template <typename T, int D>
