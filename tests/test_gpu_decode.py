@@ -93,6 +93,17 @@ def test_split_count_does_not_change_result(partition):
     assert max_err(split, oracle(args)) <= GATE[torch.float16]
 
 
+def test_split_merge_over_several_weight_windows():
+    """2188 partitions of 64 tokens: the merge holds at most 2048 partition
+    weights at a time, so it combines two windows."""
+    args = decode_inputs(torch.float16, lengths=(140000,), block_size=256, heads=2, kv_heads=1, extra_pages=1)
+    dev = to_dev(args)
+    single = paged_attention(*dev, backend="hip", partition_tokens=1 << 20)
+    split = paged_attention(*dev, backend="hip", partition_tokens=64)
+    assert (split.float() - single.float()).abs().max().item() <= 2e-3
+    assert max_err(split, oracle(args)) <= GATE[torch.float16]
+
+
 def test_hip_rejects_bad_metadata_and_noncontiguous_query():
     args = to_dev(decode_inputs(torch.float16))
     args[4][0] = 0
