@@ -85,8 +85,9 @@ struct PrefillArgs {
     const int64_t* starts;
     const int64_t* tables;
     const int64_t* lens;
-    void* ws_o;    // [T, Hq, max_chunks, D] partial outputs normalised by their sum (PartialOf<T>)
-    float* ws_ml;  // [T, Hq, max_chunks, 2] (running max in log2 units, sum)
+    void* ws_o;    // [max_chunks, T*Hq, D] partial outputs normalised by their sum (PartialOf<T>)
+    float* ws_ml;  // [max_chunks, T*Hq, 2] (running max in log2 units, sum)
+    int64_t ws_rows;  // T*Hq: one plane of partials per chunk index
     int* ws_tok;   // [T] chunks of the token's query block (written by its chunk-0 items)
     int item_stride;  // 0: one item per work-group; else items walked per work-group
     int num_seqs;
@@ -96,6 +97,7 @@ struct PrefillArgs {
     int qb;        // query tokens per item (kPfRows / group)
     int chunk;     // keys per item (multiple of kPfKeys)
     int max_chunks;
+    int chunk_choice;  // 1: a walk with more than one round of items may take a larger chunk
     int head_dim;
     int64_t num_blocks;
     int block_size;
@@ -113,19 +115,34 @@ __device__ inline int64_t block_kv_end(const PrefillArgs& a, int64_t start, int6
     return e > 0 ? e : 0;
 }
 
+// ceil(e / d) for 0 < e, d < 2^31: a float estimate of the quotient,
+// corrected to the exact ceiling with integer products -- cheaper than an
+// integer division by a run-time divisor.  The estimate's relative error is
+// a few ulps, so below 2^20 it is within one of e / d: its truncation is
+// floor(e/d) - 1, floor(e/d) or (only when that is the ceiling)
+// floor(e/d) + 1, and at most two steps up reach the ceiling.  Larger
+// quotients take the integer division.
+__device__ inline uint32_t ceil_div_u32(uint32_t e, uint32_t d) {
+    uint32_t q = (uint32_t)((float)e * __builtin_amdgcn_rcpf((float)d));
+    if (q >= (1u << 20)) return (e - 1u) / d + 1u;
+    if (q * d < e) ++q;
+    if (q * d < e) ++q;
+    return q;
+}
+
 // kv_end <= table capacity < 2^31, so 32-bit unsigned arithmetic is exact.
-__device__ inline int chunks_of(const PrefillArgs& a, int64_t kv_end) {
-    return kv_end > 0 ? (int)(((uint32_t)kv_end + (uint32_t)a.chunk - 1u) / (uint32_t)a.chunk) : 1;
+__device__ inline int chunks_of(int chunk_len, int64_t kv_end) {
+    return kv_end > 0 ? (int)ceil_div_u32((uint32_t)kv_end, (uint32_t)chunk_len) : 1;
 }
 
 // Items (query block x key chunk) of a sequence with n packed queries;
 // every query block owns at least one item so its rows always get written.
 // Without key splitting every block is exactly one item.
-__device__ inline int seq_items(const PrefillArgs& a, int64_t n, int64_t start, int64_t ctx) {
+__device__ inline int seq_items(const PrefillArgs& a, int chunk_len, int64_t n, int64_t start, int64_t ctx) {
     if (n <= 0) return 0;
     if (a.max_chunks == 1) return (int)((n + a.qb - 1) / a.qb);
     int count = 0;
-    for (int64_t b0 = 0; b0 < n; b0 += a.qb) count += chunks_of(a, block_kv_end(a, start, ctx, n, b0));
+    for (int64_t b0 = 0; b0 < n; b0 += a.qb) count += chunks_of(chunk_len, block_kv_end(a, start, ctx, n, b0));
     return count;
 }
 
@@ -136,30 +153,41 @@ template <typename T> struct PartialOf { using type = float; };
 template <> struct PartialOf<BFloat16> { using type = uint16_t; };
 
 struct PrefillItem {
-    int seq, q0, chunk, nchunks;
+    int seq, q0, chunk, nchunks, chunk_len;
     int64_t kv_end;
     int64_t row0, qlen, start, ctx;  // the sequence's metadata
 };
 
+// One sequence's metadata per lane (lane s: sequence s0 + s).
+struct SeqMeta {
+    int64_t row0, n, start, ctx;
+};
+__device__ inline SeqMeta load_meta(const PrefillArgs& a, int s) {
+    SeqMeta m{0, 0, 0, 0};
+    if (s < a.num_seqs) {
+        m.row0 = a.cu[s];
+        m.n = a.cu[s + 1] - m.row0;
+        m.start = a.starts[s];
+        m.ctx = a.lens[s];
+    }
+    return m;
+}
+
 // Item `item` -> sequence, first query token, chunk, and the sequence's
-// metadata.  Lane-parallel: each lane loads one sequence's metadata and
+// metadata, with key chunks of chunk_len keys.  `first` (optional) holds the
+// first 64 sequences' metadata, already loaded.  Lane-parallel: each lane loads one sequence's metadata and
 // counts its items, a wave prefix sum locates the sequence, the lane that
 // owns it hands its metadata over by shuffles, and that one sequence's query
 // blocks are walked.  Every wave of the work-group computes the same answer.
-__device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it, int* total_items = nullptr) {
+__device__ inline bool find_item(const PrefillArgs& a, int chunk_len, int item, PrefillItem& it,
+                                 int* total_items = nullptr, const SeqMeta* first = nullptr) {
     const int lane = __lane_id();
     int base = 0;
     bool found = false;
     for (int s0 = 0; s0 < a.num_seqs; s0 += kWave) {
-        const int s = s0 + lane;
-        int64_t row0 = 0, n = 0, start = 0, ctx = 0;
-        if (s < a.num_seqs) {
-            row0 = a.cu[s];
-            n = a.cu[s + 1] - row0;
-            start = a.starts[s];
-            ctx = a.lens[s];
-        }
-        const int cnt = seq_items(a, n, start, ctx);
+        const SeqMeta m = (first && s0 == 0) ? *first : load_meta(a, s0 + lane);
+        const int64_t row0 = m.row0, n = m.n, start = m.start, ctx = m.ctx;
+        const int cnt = seq_items(a, chunk_len, n, start, ctx);
         int incl = cnt;
 #pragma unroll
         for (int off = 1; off < kWave; off <<= 1) {
@@ -182,10 +210,11 @@ __device__ inline bool find_item(const PrefillArgs& a, int item, PrefillItem& it
             for (int64_t bi = nblocks - 1; bi >= 0; --bi) {
                 const int64_t b0 = bi * a.qb;
                 const int64_t e = block_kv_end(a, it.start, it.ctx, it.qlen, b0);
-                const int nc = chunks_of(a, e);
+                const int nc = chunks_of(chunk_len, e);
                 if (rem < nc) {
                     it.q0 = (int)b0;
                     it.chunk = rem;
+                    it.chunk_len = chunk_len;
                     it.kv_end = e;
                     it.nchunks = nc;
                     found = true;
@@ -289,7 +318,82 @@ struct PrefillLds {
     alignas(16) uint8_t v[kPfStages][kTileBytes];
     alignas(16) float b[kPfStages][kPfKeys];
     alignas(16) int full[kPfStages][kPfWaves];
+    uint64_t pick[kPfWaves];  // chunk choice: each wave's best (cost, candidate)
+    // The walk's index (num_seqs <= 64): sequence s's metadata, item count
+    // and inclusive prefix of item counts.
+    SeqMeta meta[kWave];
+    int cnt[kWave];
+    int incl[kWave];
 };
+
+// The walk's index when every sequence fits one wave (num_seqs <= 64): lane
+// s keeps sequence s's metadata, item count and inclusive prefix of counts,
+// computed once per chunk length, so that a lookup is a ballot over the
+// prefixes plus a lane-parallel search over the sequence's query blocks.
+// walk_index returns the item total; wave 0 stores the index in LDS (read
+// after the next barrier).
+__device__ inline int walk_index(const PrefillArgs& a, int chunk_len, const SeqMeta& m, PrefillLds& lds) {
+    const int lane = __lane_id();
+    const int cnt = seq_items(a, chunk_len, m.n, m.start, m.ctx);
+    int incl = cnt;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int other = __shfl_up(incl, off);
+        if (lane >= off) incl += other;
+    }
+    if (threadIdx.x < kWave) {
+        lds.meta[lane] = m;
+        lds.cnt[lane] = cnt;
+        lds.incl[lane] = incl;
+    }
+    return __shfl(incl, kWave - 1);
+}
+
+__device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, int total, const PrefillLds& lds,
+                                         int item, PrefillItem& it) {
+    if (item >= total) return false;
+    const int lane = __lane_id();
+    const SeqMeta m = lds.meta[lane];
+    const int cnt = lds.cnt[lane], incl_s = lds.incl[lane];
+    const int sel = __builtin_ctzll(__ballot(incl_s > item));
+    int rem = item - (__shfl(incl_s, sel) - __shfl(cnt, sel));
+    it.seq = sel;
+    it.row0 = __shfl(m.row0, sel);
+    it.qlen = __shfl(m.n, sel);
+    it.start = __shfl(m.start, sel);
+    it.ctx = __shfl(m.ctx, sel);
+    it.chunk_len = chunk_len;
+    // Query blocks from the last to the first (as find_item), 64 at a time:
+    // lane l takes the l-th block of the group.
+    const int64_t nblocks = (it.qlen + a.qb - 1) / a.qb;
+    for (int64_t g0 = 0; g0 < nblocks; g0 += kWave) {
+        const int64_t bi = nblocks - 1 - (g0 + lane);
+        int64_t e = 0;
+        int nc = 0;
+        if (bi >= 0) {
+            e = block_kv_end(a, it.start, it.ctx, it.qlen, bi * a.qb);
+            nc = chunks_of(chunk_len, e);
+        }
+        int incl = nc;
+#pragma unroll
+        for (int off = 1; off < kWave; off <<= 1) {
+            const int other = __shfl_up(incl, off);
+            if (lane >= off) incl += other;
+        }
+        const int group = __shfl(incl, kWave - 1);
+        if (rem < group) {
+            const int l = __builtin_ctzll(__ballot(incl > rem));
+            it.q0 = (int)((nblocks - 1 - (g0 + l)) * a.qb);
+            it.chunk = rem - (__shfl(incl, l) - __shfl(nc, l));
+            it.kv_end = __shfl(e, l);
+            it.nchunks = __shfl(nc, l);
+            return true;
+        }
+        rem -= group;
+    }
+    return false;  // (only if the counts are inconsistent)
+}
+
 
 // One work item, computed by the whole work-group.
 template <typename T, int PAGES>
@@ -324,8 +428,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         (int)(item.start < -1 ? -1 : (item.start > cap ? (int64_t)cap : item.start)));
     const int64_t* table = a.tables + (int64_t)seq * a.table_width;
     const int kv_end = (int)kv_end64;
-    const int chunk_start = chunk * a.chunk;
-    const int chunk_end = min(chunk_start + a.chunk, kv_end);
+    const int chunk_len = __builtin_amdgcn_readfirstlane(item.chunk_len);
+    const int chunk_start = chunk * chunk_len;
+    const int chunk_end = min(chunk_start + chunk_len, kv_end);
     const int t_begin = chunk_start / kPfKeys;
     const int t_end = chunk_end > chunk_start ? (chunk_end + kPfKeys - 1) / kPfKeys : t_begin;
 
@@ -700,7 +805,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * lg) = w;
             }
         } else {
-            const int64_t slot = rowid * a.max_chunks + chunk;
+            const int64_t slot = (int64_t)chunk * a.ws_rows + rowid;
             const float inv = (row_ok[nb] && l_row > 0.f) ? 1.f / l_row : 0.f;
             using P = typename PartialOf<T>::type;
             P* po = static_cast<P*>(a.ws_o) + slot * kPfD;
@@ -727,6 +832,90 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     }
 }
 
+// Chunk choice for a walk (the caller's chunk is the smallest allowed: it
+// bounds the workspace).  The best chunk puts the item count just under a
+// multiple of the walkers, and which chunk that is depends on the lengths,
+// which only the device sees.  Every work-group evaluates the same 128
+// candidates a.chunk + 64*step*c (c < 128, up to the capacity) against the
+// same estimate of the makespan (in tile times) of walking one kv head's
+// items with W work-groups:
+//   max(ceil(items / W) * (F + chunk / 64), (tiles + F * items) / W),
+// rounds of full items, never below the perfectly balanced total, with F
+// the fixed cost of an item (start-up and partial stores, about 2.5 tile
+// times), and all take the cheapest (ties: the smaller chunk).  Thread t
+// counts candidate t % 128 over every fourth query block (t / 128 picks
+// which), so the count costs a quarter of the blocks per thread; the sums
+// meet in the K ring, which the first copies fill only after the final
+// barrier here.
+constexpr float kItemFixedTiles = 2.5f;
+constexpr int kChoiceCands = 128;
+constexpr int kChoiceSlices = kPfThreads / kChoiceCands;
+
+__device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta& first) {
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int ci = tid % kChoiceCands, slice = tid / kChoiceCands;
+    const int cap = a.table_width * a.block_size;
+    const int cmax = (cap + kPfKeys - 1) / kPfKeys * kPfKeys;
+    const int span = (cmax - a.chunk) / kPfKeys;  // candidate steps above the minimum
+    const int step = max(1, (span + kChoiceCands - 1) / kChoiceCands);
+    const int cand = a.chunk + kPfKeys * step * ci;
+    const bool valid = cand <= cmax;  // candidate 0, the minimum, always is
+    uint32_t items = 0, tiles = 0;
+    if (__builtin_amdgcn_ballot_w64(valid) != 0) {  // wave-uniform
+        int blk = 0;  // query blocks of the sequences before (uniform)
+        for (int s0 = 0; s0 < a.num_seqs; s0 += kWave) {
+            // One sequence's metadata per lane, then every lane walks them all.
+            const SeqMeta m = s0 == 0 ? first : load_meta(a, s0 + lane);
+            const int64_t n = m.n, start = m.start, ctx = m.ctx;
+            const int cnt = min(kWave, a.num_seqs - s0);
+            for (int j = 0; j < cnt; ++j) {
+                const int64_t nj = __shfl(n, j), sj = __shfl(start, j), cj = __shfl(ctx, j);
+                const int nb = nj > 0 ? (int)((nj + a.qb - 1) / a.qb) : 0;
+                for (int k = ((slice - blk) % kChoiceSlices + kChoiceSlices) % kChoiceSlices; k < nb;
+                     k += kChoiceSlices) {
+                    const uint32_t e = (uint32_t)block_kv_end(a, sj, cj, nj, (int64_t)k * a.qb);
+                    items += e > 0 ? ceil_div_u32(e, (uint32_t)cand) : 1;
+                    tiles += (e + kPfKeys - 1) / kPfKeys;
+                }
+                blk += nb;
+            }
+        }
+    }
+    uint32_t* sc_items = reinterpret_cast<uint32_t*>(&lds.k[0][0]);  // [slice][candidate]
+    uint32_t* sc_tiles = sc_items + kChoiceSlices * kChoiceCands;     // [slice]
+    sc_items[slice * kChoiceCands + ci] = items;
+    if (ci == 0) sc_tiles[slice] = tiles;
+    __syncthreads();
+    uint64_t key = ~0ull;
+    if (slice == 0 && valid) {
+        uint32_t it_sum = 0, tl_sum = 0;
+#pragma unroll
+        for (int k = 0; k < kChoiceSlices; ++k) {
+            it_sum += sc_items[k * kChoiceCands + ci];
+            tl_sum += sc_tiles[k];
+        }
+        const uint32_t w = (uint32_t)a.item_stride;
+        const float rounds = (float)((it_sum + w - 1) / w);
+        const float cost = fmaxf(rounds * (kItemFixedTiles + (float)(cand / kPfKeys)),
+                                 ((float)tl_sum + kItemFixedTiles * (float)it_sum) / (float)w);
+        // Non-negative floats order like their bit patterns.
+        key = ((uint64_t)__float_as_uint(cost) << 32) | (uint32_t)ci;
+    }
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), off) << 32) |
+                           (uint32_t)__shfl_xor((int)(uint32_t)key, off);
+        key = o < key ? o : key;
+    }
+    if (lane == 0) lds.pick[wave] = key;
+    __syncthreads();
+    uint64_t best = lds.pick[0];
+#pragma unroll
+    for (int w = 1; w < kPfWaves; ++w) best = lds.pick[w] < best ? lds.pick[w] : best;
+    __syncthreads();  // every thread has read the sums and picks before the ring is refilled
+    return a.chunk + kPfKeys * step * (int)(uint32_t)best;
+}
+
 // Items are enumerated densely.  WALK = false: one item per work-group (the
 // grid covers every possible item; work-groups past the end exit).  WALK =
 // true: one work-group per CU slot, each walking items idx, idx +
@@ -737,7 +926,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
     __shared__ __attribute__((aligned(16))) PrefillLds lds;
     if constexpr (!WALK) {
         PrefillItem item;
-        if (!find_item(a, blockIdx.x / a.kv_heads, item)) return;
+        if (!find_item(a, a.chunk, blockIdx.x / a.kv_heads, item)) return;
         prefill_item<T, PAGES>(a, item, lds);
     } else {
         // The first lookup also counts the items, so that the walk ends
@@ -745,13 +934,37 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
         int total = 0;
         int idx = blockIdx.x / a.kv_heads;
         PrefillItem item;
-        bool ok = find_item(a, idx, item, &total);
+        // Up to 64 sequences: their metadata and item counts go to LDS once,
+        // and every lookup reads them there (nothing held in registers
+        // across the tile loop).
+        const bool indexed = a.num_seqs <= kWave;
+        int chunk_len = a.chunk;
+        bool ok = false;
+        if (indexed) {
+            const SeqMeta m = load_meta(a, (int)(threadIdx.x & (kWave - 1)));
+            total = walk_index(a, chunk_len, m, lds);
+            if (a.chunk_choice && total > a.item_stride) {
+                // More than one round of items: the lengths decide the chunk.
+                chunk_len = choose_chunk(a, lds, m);
+                total = walk_index(a, chunk_len, m, lds);
+            }
+            __syncthreads();  // the index is in LDS
+            ok = find_item_indexed(a, chunk_len, total, lds, idx, item);
+        } else {
+            ok = find_item(a, chunk_len, idx, item, &total);
+            if (a.chunk_choice && total > a.item_stride) {
+                const SeqMeta m = load_meta(a, (int)(threadIdx.x & (kWave - 1)));
+                chunk_len = choose_chunk(a, lds, m);
+                ok = find_item(a, chunk_len, idx, item, &total);
+            }
+        }
         while (ok) {
             prefill_item<T, PAGES>(a, item, lds);
             idx += a.item_stride;
             if (idx >= total) break;
             __syncthreads();  // every wave is done with the LDS ring before the next item refills it
-            ok = find_item(a, idx, item);
+            ok = indexed ? find_item_indexed(a, chunk_len, total, lds, idx, item)
+                         : find_item(a, chunk_len, idx, item);
         }
     }
 }
@@ -774,8 +987,8 @@ __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(Pref
     for (int idx = threadIdx.x; idx < a.q_heads * (kPfD / 8); idx += kMergeThreads) {
         const int head = idx / (kPfD / 8);
         const int d0 = 8 * (idx % (kPfD / 8));
-        const int64_t slot0 = (token * a.q_heads + head) * a.max_chunks;
-        const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + slot0;
+        const int64_t rowid = token * a.q_heads + head;  // chunk c's slot: c * ws_rows + rowid
+        const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + rowid;
         // One pass: every load of a group of chunks is in flight together,
         // and the running reference moves (with a rescale) only when a
         // group holds a larger maximum.
@@ -792,10 +1005,11 @@ __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(Pref
 #pragma unroll
             for (int k = 0; k < kGroup; ++k) {
                 const int c = min(c0 + k, nchunks - 1);
-                const u32x4* po = reinterpret_cast<const u32x4*>(static_cast<const P*>(a.ws_o) + (slot0 + c) * kPfD + d0);
+                const int64_t slot = (int64_t)c * a.ws_rows + rowid;
+                const u32x4* po = reinterpret_cast<const u32x4*>(static_cast<const P*>(a.ws_o) + slot * kPfD + d0);
                 raw[k][0] = po[0];
                 if constexpr (sizeof(P) == 4) raw[k][1] = po[1];
-                mlc[k] = ml[c];
+                mlc[k] = ml[(int64_t)c * a.ws_rows];
             }
             f32x4 x[kGroup][2];
 #pragma unroll
@@ -971,9 +1185,11 @@ struct PrefillPlan {
 constexpr int64_t kPrefillCUs = 256;
 
 // Host plan from shapes only (lengths stay on the device).  Enough query
-// blocks to occupy the GPU twice over: no key split.  Otherwise split the
-// keys into chunks of at least 512 (and at most 16 chunks per block), which
-// spreads long contexts over all CUs at the cost of partials and a merge.
+// blocks to occupy the GPU 1.5 times over: no key split.  Otherwise split
+// the keys into chunks of at least 512 (and at most 32 chunks per block,
+// which bounds the workspace), which spreads long contexts over all CUs at
+// the cost of partials and a merge; a walk over more than one round of
+// items then takes a larger chunk on the device when the lengths favour it.
 PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64_t kv_heads,
                               int64_t head_dim, int64_t block_size, int64_t table_width, int64_t chunk_tokens) {
     PrefillPlan p{};
@@ -986,8 +1202,12 @@ PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_
     const int64_t blocks_bound = (total_tokens + p.qb - 1) / p.qb + num_seqs;
     int64_t chunk;
     if (chunk_tokens > 0) chunk = (chunk_tokens + kPfKeys - 1) / kPfKeys * kPfKeys;
-    else if (blocks_bound * kv_heads >= kPrefillCUs + kPrefillCUs / 2) chunk = cap_tiles;
-    else chunk = std::max<int64_t>(512, ((cap + 15) / 16 + kPfKeys - 1) / kPfKeys * kPfKeys);
+    // The split test counts the query blocks the tokens fill at least (the
+    // bound above adds one partial block per sequence): near the threshold,
+    // ragged contexts make whole-context items uneven, and the walk's chunk
+    // choice can still take chunks as long as the capacity.
+    else if ((total_tokens + p.qb - 1) / p.qb * kv_heads >= kPrefillCUs + kPrefillCUs / 2) chunk = cap_tiles;
+    else chunk = std::max<int64_t>(512, ((cap + 31) / 32 + kPfKeys - 1) / kPfKeys * kPfKeys);
     if (chunk > cap_tiles) chunk = cap_tiles;
     if (chunk < kPfKeys) chunk = kPfKeys;
     p.chunk = (int)chunk;
@@ -1065,6 +1285,8 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         a.qb = p.qb;
         a.chunk = p.chunk;
         a.max_chunks = p.max_chunks;
+        a.ws_rows = total_tokens * q_heads;
+        a.chunk_choice = chunk_tokens <= 0 ? 1 : 0;
         if (need > 0) {
             a.ws_o = workspace;
             a.ws_ml = static_cast<float*>(workspace) + total_tokens * q_heads * p.max_chunks * kPfD;

@@ -228,3 +228,36 @@ def test_prefill_work_groups_walk_several_items(dtype, block_size, chunk_tokens)
     actual = paged_prefill_attention(*args, block_size, backend="hip", chunk_tokens=chunk_tokens)
     expected = paged_oracle.paged_prefill_attention(*[a.cpu() for a in args], block_size, cast=False)
     assert max_err(actual, expected) <= GATE[dtype]
+
+
+@pytest.mark.parametrize("chunk_tokens", [0, 512])
+def test_prefill_walk_over_more_than_64_sequences(chunk_tokens):
+    """70 sequences of 8 new tokens (GQA group 8, so 32 tokens per query
+    block) after 500..3000 prior tokens: the keys split, the work-groups walk
+    several items each, and with more than 64 sequences the lookups take the
+    general path; with chunk_tokens=0 the walk also picks its chunk from the
+    lengths."""
+    dtype, block, heads, kv_heads = torch.bfloat16, 16, 16, 2
+    gen = torch.Generator().manual_seed(70)
+    seqs, new = 70, 8
+    priors = torch.randint(500, 3001, (seqs,), generator=gen)
+    widths = (priors + new + block - 1) // block
+    width = int(widths.max())
+    pages = int(widths.sum()) + 3
+    kc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
+    vc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
+    perm = torch.randperm(pages, generator=gen)
+    tables = torch.full((seqs, width), -1, dtype=torch.int64)
+    used = 0
+    for s in range(seqs):
+        w = int(widths[s])
+        tables[s, :w] = perm[used:used + w]
+        used += w
+    cu = torch.arange(0, (seqs + 1) * new, new, dtype=torch.int64)
+    starts = priors.to(torch.int64)
+    lens = starts + new
+    q = torch.randn(seqs * new, heads, 128, generator=gen).to(dtype)
+    args = [q, kc, vc, cu, starts, tables, lens]
+    actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip", chunk_tokens=chunk_tokens)
+    expected = paged_oracle.paged_prefill_attention(*args, block, cast=False)
+    assert max_err(actual, expected) <= GATE[dtype]
