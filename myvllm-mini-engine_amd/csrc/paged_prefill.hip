@@ -207,6 +207,18 @@ __device__ inline bool find_item(const PrefillArgs& a, int chunk_len, int item, 
             // Query blocks from the last (longest key range) to the first, so
             // that the work-groups dispatched last are the short ones.
             const int64_t nblocks = (it.qlen + a.qb - 1) / a.qb;
+            it.chunk_len = chunk_len;
+            if (a.max_chunks == 1) {  // one item per block: no search
+                const int64_t b0 = (nblocks - 1 - rem) * a.qb;
+                it.q0 = (int)b0;
+                it.chunk = 0;
+                it.kv_end = block_kv_end(a, it.start, it.ctx, it.qlen, b0);
+                it.nchunks = 1;
+                found = true;
+                if (!total_items) return true;
+                base += total;
+                continue;
+            }
             for (int64_t bi = nblocks - 1; bi >= 0; --bi) {
                 const int64_t b0 = bi * a.qb;
                 const int64_t e = block_kv_end(a, it.start, it.ctx, it.qlen, b0);
