@@ -173,13 +173,18 @@ __global__ __launch_bounds__(kVecThreads) void qk_norm_rope_vec_kernel(RopeArgs 
     const int h = is_q ? r : is_k ? r - a.q_heads : r - a.q_heads - a.kv_heads;
     const uint16_t* src = is_q ? a.q + t * a.q_stride : is_k ? a.k + t * a.k_stride : a.v + t * a.v_stride;
     src += (int64_t)h * kDim + sub * 8;
-    const int64_t slot = live && !is_q ? rope_slot(a, t) : -1;
     const u32x4 zero = {0u, 0u, 0u, 0u};
-    const u32x4 xv = live ? *reinterpret_cast<const u32x4*>(src) : zero;
+    // Lanes past the last row read row 0 of q (in bounds) and discard it: an
+    // unconditional load keeps all loads in flight together.
+    const u32x4 xraw = *reinterpret_cast<const u32x4*>(src);
+    const u32x4 xv = live ? xraw : zero;
     const u32x4 wv = *reinterpret_cast<const u32x4*>((is_q ? a.q_weight : a.k_weight) + sub * 8);
     const int64_t trig = (int64_t)t * (kDim / 2) + (sub % kHalfLanes) * 8;
     const u32x4 cv = *reinterpret_cast<const u32x4*>(a.cos + trig);
     const u32x4 sv = *reinterpret_cast<const u32x4*>(a.sin + trig);
+    // The cache slot (one or two dependent metadata loads) after the row
+    // loads, so that their latencies overlap instead of adding up.
+    const int64_t slot = live && !is_q ? rope_slot(a, t) : -1;
 
     float x[8];
 #pragma unroll
