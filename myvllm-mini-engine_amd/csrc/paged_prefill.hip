@@ -88,6 +88,7 @@ struct PrefillArgs {
     void* ws_o;    // [max_chunks, T*Hq, D] partial outputs normalised by their sum (PartialOf<T>)
     float* ws_ml;  // [max_chunks, T*Hq, 2] (running max in log2 units, sum)
     int64_t ws_rows;  // T*Hq: one plane of partials per chunk index
+    int64_t total_tokens;  // T: packed query rows (every row a sequence covers lies below it)
     int* ws_tok;   // [T] chunks of the token's query block (written by its chunk-0 items)
     int item_stride;  // 0: one item per work-group; else items walked per work-group
     int num_seqs;
@@ -162,11 +163,16 @@ struct PrefillItem {
 struct SeqMeta {
     int64_t row0, n, start, ctx;
 };
+// Offsets are clamped to the packed rows, so that metadata that is not
+// monotone (unchecked in trusted mode) can neither send a write past the
+// output nor make a lookup loop over an absurd number of query blocks.
 __device__ inline SeqMeta load_meta(const PrefillArgs& a, int s) {
     SeqMeta m{0, 0, 0, 0};
     if (s < a.num_seqs) {
-        m.row0 = a.cu[s];
-        m.n = a.cu[s + 1] - m.row0;
+        const int64_t lo = min(max(a.cu[s], (int64_t)0), a.total_tokens);
+        const int64_t hi = min(max(a.cu[s + 1], lo), a.total_tokens);
+        m.row0 = lo;
+        m.n = hi - lo;
         m.start = a.starts[s];
         m.ctx = a.lens[s];
     }
@@ -1298,6 +1304,7 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         a.chunk = p.chunk;
         a.max_chunks = p.max_chunks;
         a.ws_rows = total_tokens * q_heads;
+        a.total_tokens = total_tokens;
         a.chunk_choice = chunk_tokens <= 0 ? 1 : 0;
         if (need > 0) {
             a.ws_o = workspace;

@@ -261,3 +261,23 @@ def test_prefill_walk_over_more_than_64_sequences(chunk_tokens):
     actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip", chunk_tokens=chunk_tokens)
     expected = paged_oracle.paged_prefill_attention(*args, block, cast=False)
     assert max_err(actual, expected) <= GATE[dtype]
+
+
+def test_trusted_mode_offsets_out_of_order_stay_in_bounds():
+    """validate=False with query offsets that are not monotone or pass the
+    packed rows: the kernel clamps them to the rows, so it neither writes
+    past the output nor loops over absurd block counts; rows no sequence
+    covers are unspecified, every value finite."""
+    dtype, block = torch.bfloat16, 16
+    gen = torch.Generator().manual_seed(5)
+    kc = torch.randn(40, block, 8, 128, generator=gen).to(dtype).to(DEV)
+    vc = torch.randn(40, block, 8, 128, generator=gen).to(dtype).to(DEV)
+    tables = torch.randperm(40, generator=gen)[:36].view(3, 12).to(DEV)
+    q = torch.randn(71, 16, 128, generator=gen).to(dtype).to(DEV)
+    starts = torch.tensor([90, 3, 10], device=DEV)
+    lens = torch.tensor([140, 50, 100], device=DEV)
+    for cu in ([0, 50, 30, 71], [0, 50, 1 << 40, 71], [-5, 20, 60, 1 << 33]):
+        out = paged_prefill_attention(q, kc, vc, torch.tensor(cu, device=DEV), starts, tables, lens, block,
+                                      backend="hip", validate=False)
+        torch.cuda.synchronize()
+        assert out.shape == q.shape
