@@ -176,9 +176,11 @@ def decode_attention_block_step(args, torch, layers, paged_attention, cpu):
     """The attention block of the decode step for all 28 headline layers in one captured graph:
     per layer the fused q/k RMSNorm + RoPE + KV page write of the new token (replacing q_norm,
     k_norm, apply_rope and write_kv_cache_batch, native_qwen3.py:179-191), paged attention over
-    the updated context, and the o_proj GEMV (hipBLASLt through torch.mm; native_qwen3.py:197).
+    the updated context, and the o_proj projection of the batch (mvme_linear_rows, HipLinear's
+    decode-batch kernel; native_qwen3.py:197).
     Inputs are synthetic QKV projections of the batch; reuses the headline layers' caches."""
     from mini_engine_hip.kernels.rope import qk_norm_rope_write_kv
+    from mini_engine_hip.kernels.linear import linear_rows
 
     hidden = 2048
     gen = torch.Generator(device="cuda").manual_seed(BASE_SEED + 99)
@@ -188,7 +190,7 @@ def decode_attention_block_step(args, torch, layers, paged_attention, cpu):
         c["wk"] = (torch.rand((D,), generator=gen, device="cuda") + 0.5).half()
         angles = torch.randn((BATCH, D // 2), generator=gen, device="cuda")
         c["cos"], c["sin"] = angles.cos().half(), angles.sin().half()
-        c["w_o"] = (torch.randn((HQ * D, hidden), generator=gen, device="cuda") * 0.02).half()
+        c["w_o"] = (torch.randn((hidden, HQ * D), generator=gen, device="cuda") * 0.02).half()  # [out, in]
         c["positions"] = (c["context_lens"] - 1).contiguous()
         c["q_rot"] = torch.empty((BATCH, HQ, D), dtype=torch.float16, device="cuda")
         c["hidden"] = torch.empty((BATCH, hidden), dtype=torch.float16, device="cuda")
@@ -207,7 +209,7 @@ def decode_attention_block_step(args, torch, layers, paged_attention, cpu):
                                   out=c["q_rot"])
             paged_attention(c["q_rot"], c["key_cache"], c["value_cache"], c["block_tables"], c["context_lens"],
                             BLOCK, backend="hip", validate=False, out=c["out"])
-            torch.mm(c["out"].view(BATCH, HQ * D), c["w_o"], out=c["hidden"])
+            linear_rows(c["out"].view(BATCH, HQ * D), c["w_o"], out=c["hidden"])
 
     ms, _ = graph_time_ms(step, torch, calls_per_graph=3 * LAYERS, replays=args.steps, warmup=args.warmup)
     # Layer 0 against the reference: the rotated q, the written K/V rows, attention, o_proj.
@@ -225,7 +227,7 @@ def decode_attention_block_step(args, torch, layers, paged_attention, cpu):
         tensors = {"query": c["q_rot"].cpu(), "key_cache": kc, "value_cache": vc, "block_tables": tables,
                    "context_lens": c["context_lens"].cpu()}
         attn_err = max_abs(c["out"], cpu.decode(tensors, BLOCK))
-        o_err = max_abs(c["hidden"], c["out"].float().cpu().view(BATCH, -1) @ c["w_o"].float().cpu())
+        o_err = max_abs(c["hidden"], c["out"].float().cpu().view(BATCH, -1) @ c["w_o"].float().cpu().t())
         passed = v_exact and rope_err <= 4e-3 and attn_err <= 2e-3 and o_err <= 2e-2
     for c in layers:
         for key in ("qkv", "wq", "wk", "cos", "sin", "w_o", "positions", "q_rot", "hidden"):
@@ -477,6 +479,7 @@ def _extra_norm_rope(torch, cpu_leg, dev, extra):
     four steps as separate eager torch ops plus the HIP scatter (the reference's torch data path, timed
     eagerly on the stream, not captured)."""
     from mini_engine_hip.kernels.rope import qk_norm_rope_write_kv
+    from mini_engine_hip.kernels.linear import linear_rows
     from mini_engine_hip.kernels.data import write_kv_cache_slots
 
     for name, tokens, dtype, mode in (("norm_rope_kv_write_prefill_1024tok_bf16", 1024, torch.bfloat16, "slots"),
@@ -552,29 +555,46 @@ def _extra_norm_rope(torch, cpu_leg, dev, extra):
 
 
 def _extra_after_attention(torch, cpu, dev, extra):
-    """The step after attention at the headline batch: o_proj GEMV (a library GEMM, hipBLASLt
-    through torch.mm, as the reference's CudaLinear uses cuBLAS) and greedy argmax over a
-    151,936-entry vocabulary (the HIP kernel), 32 sequences, hidden 2048."""
+    """The step after attention at the headline batch: the o_proj projection of 32 rows over 28
+    layers' distinct weights (the reference's CudaLinear -- torch.mm(x, weight.t()) on the
+    [out, in] weight, a library GEMM -- beside mvme_linear_rows, HipLinear's decode-batch kernel)
+    and greedy argmax over a 151,936-entry vocabulary (the HIP kernel), 32 sequences, hidden 2048."""
     from mini_engine_hip.sampling import greedy_argmax
+    from mini_engine_hip.kernels.linear import linear_rows
 
     batch, hidden, vocab = BATCH, 2048, 151936
     gen = torch.Generator().manual_seed(BASE_SEED + 11)
     attn = torch.randn(batch, HQ * D, generator=gen).to(torch.bfloat16).to(dev)
-    w_t = (torch.randn(HQ * D, hidden, generator=gen) * 0.02).to(torch.bfloat16).to(dev)   # o_proj.weight^T
-    out_o = torch.empty(batch, hidden, dtype=torch.bfloat16, device=dev)
+    dgen = torch.Generator(device=dev).manual_seed(BASE_SEED + 12)
+    weights = [(torch.randn(hidden, HQ * D, generator=dgen, device=dev) * 0.02).to(torch.bfloat16)
+               for _ in range(LAYERS)]  # o_proj.weight of each layer, [out, in]
+    out_lib = torch.empty(batch, hidden, dtype=torch.bfloat16, device=dev)
+    out_hip = torch.empty(batch, hidden, dtype=torch.bfloat16, device=dev)
 
     def many(fn, n):
         def run():
             for _ in range(n):
                 fn()
         return run
-    ms, _ = graph_time_ms(many(lambda: torch.mm(attn, w_t, out=out_o), 50), torch, calls_per_graph=50,
-                          replays=20, warmup=3)
+
+    def layers(fn):
+        def run():
+            for w in weights:
+                fn(w)
+        return run
+    ms_lib, _ = graph_time_ms(layers(lambda w: torch.mm(attn, w.t(), out=out_lib)), torch, calls_per_graph=LAYERS,
+                              replays=20, warmup=3)
+    ms_hip, _ = graph_time_ms(layers(lambda w: linear_rows(attn, w, out=out_hip)), torch, calls_per_graph=LAYERS,
+                              replays=20, warmup=3)
     o_bytes = HQ * D * hidden * 2 + batch * HQ * D * 2 + batch * hidden * 2
-    o_ref = attn.float().cpu() @ w_t.float().cpu()
-    extra["o_proj_gemv_b32_2048x2048_bf16"] = {
-        "us_per_call": ms / 50 * 1e3, "GBps": o_bytes / (ms / 50 * 1e-3) / 1e9, "library": "hipBLASLt (torch.mm)",
-        "max_abs_error_vs_fp32": max_abs(out_o, o_ref)}
+    o_ref = attn.float().cpu() @ weights[-1].float().cpu().t()
+    per_hip, per_lib = ms_hip / LAYERS * 1e-3, ms_lib / LAYERS * 1e-3
+    extra["o_proj_b32_2048x2048_bf16_28_weights"] = {
+        "us_per_call": per_hip * 1e6, "GBps": o_bytes / per_hip / 1e9,
+        "frac_of_hbm_peak": o_bytes / per_hip / 1e9 / HBM_PEAK_GBS,
+        "kernel": "mvme_linear_rows", "max_abs_error_vs_fp32": max_abs(out_hip, o_ref),
+        "library_torch_mm_us_per_call": per_lib * 1e6, "library_max_abs_error_vs_fp32": max_abs(out_lib, o_ref)}
+    del weights
     for dtype, name in ((torch.bfloat16, "greedy_argmax_b32_vocab151936_bf16"),
                         (torch.float32, "greedy_argmax_b32_vocab151936_fp32")):
         logits = torch.randn(batch, vocab, generator=gen).to(dtype).to(dev)

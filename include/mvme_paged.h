@@ -240,6 +240,21 @@ int mvme_greedy_argmax(int64_t* out, const void* logits, int64_t batch, int64_t 
                        int64_t row_stride, int dtype, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/*
+ * Linear layer for at most 64 rows (the decode batch): out[m, n] =
+ * sum_k x[m * x_row_stride + k] * weight[n * in_features + k] (+ bias[n]),
+ * weight in nn.Linear's [out_features, in_features] layout, fp32
+ * accumulation, one rounding to dtype (MVME_FP16 / MVME_BF16).
+ * in_features a multiple of 32, out_features a multiple of 16, x and weight
+ * 16-byte aligned, out 8-byte aligned; rows = 0 is a no-op.  No workspace.
+ * Replaces, for rows <= 64: CudaLinear.forward's torch.mm(x, weight.t())
+ *   (mini_engine/kernels/linear.py:14-30), the attention output projection
+ *   of the decode step (self.o_proj, mini_engine/model/native_qwen3.py:197).
+ */
+int mvme_linear_rows(void* out, const void* x, const void* weight, const void* bias, int64_t rows,
+                     int64_t in_features, int64_t out_features, int64_t x_row_stride, int dtype,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

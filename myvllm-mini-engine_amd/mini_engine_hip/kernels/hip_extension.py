@@ -43,6 +43,7 @@ SIGNATURES = {
                                           ctypes.c_float, _int, _vp]),
     "mvme_greedy_argmax_workspace_size": (_size, [_i64, _i64]),
     "mvme_greedy_argmax": (_int, [_vp, _vp, _i64, _i64, _i64, _int, _vp, _size, _vp]),
+    "mvme_linear_rows": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
 }
 
 

@@ -192,3 +192,14 @@ def test_greedy_sampling_contract_on_cpu():
         sample_next_token(x[0])
     with pytest.raises(RuntimeError, match="contiguous CUDA"):
         sample_next_token(x)
+
+
+def test_hip_linear_contract_on_cpu():
+    """tests/test_prefill_linear_chat.py:22-29 for HipLinear: CPU input is refused."""
+    from mini_engine_hip.kernels.linear import HipLinear, linear_rows
+
+    x = torch.randn(2, 3, 7)
+    with pytest.raises(ValueError, match="CUDA"):
+        HipLinear(7, 5)(x)
+    with pytest.raises(ValueError, match="CUDA"):
+        linear_rows(torch.randn(2, 64), torch.randn(16, 64))
