@@ -648,6 +648,11 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             lookup(tp + 2 + k);
             issue(tp + 2 + k, (st0 + 2 + k) & (kPfStages - 1));
         }
+        // Unrolled: with this loop left rolled, the compiler's wait insertion
+        // puts a full vmcnt(0) at its head (before the first product of every
+        // tile), and that wait also covers the copies issued just above, so
+        // each pair of tiles would wait for the next pair to land.
+#pragma unroll
         for (int k = 0; k < 2 && tp + k < t_end; ++k) {
             const int tile = tp + k;
             const int st = (st0 + k) & (kPfStages - 1);
@@ -678,6 +683,10 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     // matrix core forwards a result straight into the next
                     // product of the same accumulator, while alternating between
                     // accumulators costs issue slots.
+                    // Raised wave priority over the matrix products: while a wave
+                    // issues MFMAs, the other wave of its SIMD runs softmax VALU
+                    // work in the gaps rather than competing for the same slots.
+                    __builtin_amdgcn_s_setprio(1);
                     u32x4 kop[2][4];
 #pragma unroll
                     for (int dc = 0; dc < 4; ++dc) {
@@ -696,6 +705,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     // Scores -> probabilities against the running reference m_run.
                     // Fast tiles keep raw scores and scale inside the exponent;
                     // edge tiles are scaled, biased and masked in place first.
+                    __builtin_amdgcn_s_setprio(0);
                     if (!fast) {
 #pragma unroll
                         for (int nb = 0; nb < kPfNb; ++nb) {
@@ -788,6 +798,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                         vop[h] = u32x4{w0[0], w0[1], w1[0], w1[1]};
                     }
                 };
+                __builtin_amdgcn_s_setprio(1);
                 u32x4 vcur[2], vnext[2];
                 vread(0, vcur);
 #pragma unroll
@@ -802,6 +813,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     vcur[0] = vnext[0];
                     vcur[1] = vnext[1];
                 }
+                __builtin_amdgcn_s_setprio(0);
             }
         }
     }
