@@ -66,12 +66,13 @@ struct DecodeArgs {
 };
 
 // K/V rows are read once per call, by one work-group.  When a call's rows
-// can exceed the caches (16-wave whole-sequence mode and more than 64 MiB of
-// K/V within the tables' capacity) the loads carry the non-temporal hint
-// (`nt`), so that streamed rows do not displace cache lines that are reused
-// (page tables, the query, rows other waves still need): on the 28-layer
-// B32 / ctx 2048 fp16 headline step a call went from 49.7 to 45.4 us and the
-// ragged B64 case from 99.7 to 93.7 us.  Smaller calls keep ordinary loads,
+// can exceed the caches (more than 64 MiB of K/V within the tables'
+// capacity) the loads carry the non-temporal hint (`nt`), so that streamed
+// rows do not displace cache lines that are reused (page tables, the query,
+// rows other waves still need): on the 28-layer B32 / ctx 2048 fp16 headline
+// step a call went from 49.7 to 45.4 us, the ragged B64 case from 99.7 to
+// 93.7 us, and split-K calls of 512 MiB (B1 / ctx 128k, B4 / ctx 32k,
+// B16 / ctx 8k, bf16) from 101-106 to 89-94 us.  Smaller calls keep ordinary loads,
 // so that their rows can stay cached from one call to the next: with the
 // hint a repeated B8 / ctx 512 bf16 call (16 MiB) went from 10.4 to 11.7 us.
 template <bool STREAM>
@@ -494,7 +495,7 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     }
     p.partition = (int)part;
     p.max_parts = (int)((cap + part - 1) / part);
-    p.stream = p.waves == kWholeWaves && batch * cap * kv_heads * head_dim * 4 > kStreamBytes;
+    p.stream = batch * cap * kv_heads * head_dim * 4 > kStreamBytes;
     return p;
 }
 
@@ -506,15 +507,12 @@ void launch_decode_kernel(const DecodeArgs& a, dim3 grid, bool page_uniform, hip
         hipLaunchKernelGGL((paged_decode_kernel<T, D, G, false, NW, STREAM>), grid, dim3(NW * kWave), 0, s, a);
 }
 
-// Streaming loads exist for the 16-wave mode only.
 template <typename T, int D, int G, int NW>
 void launch_decode_nw(const DecodeArgs& a, int units, bool page_uniform, bool stream, hipStream_t s) {
     const dim3 grid(units, a.max_parts);
-    if constexpr (NW == kWholeWaves) {
-        if (stream) {
-            launch_decode_kernel<T, D, G, NW, true>(a, grid, page_uniform, s);
-            return;
-        }
+    if (stream) {
+        launch_decode_kernel<T, D, G, NW, true>(a, grid, page_uniform, s);
+        return;
     }
     launch_decode_kernel<T, D, G, NW, false>(a, grid, page_uniform, s);
 }
@@ -522,7 +520,7 @@ void launch_decode_nw(const DecodeArgs& a, int units, bool page_uniform, bool st
 template <typename T, int D, int G>
 void launch_decode(const DecodeArgs& a, const DecodePlan& p, int units, bool page_uniform, hipStream_t s) {
     if (p.waves == kWholeWaves) launch_decode_nw<T, D, G, kWholeWaves>(a, units, page_uniform, p.stream, s);
-    else launch_decode_nw<T, D, G, kSplitWaves>(a, units, page_uniform, false, s);
+    else launch_decode_nw<T, D, G, kSplitWaves>(a, units, page_uniform, p.stream, s);
     if (a.max_parts > 1)
         hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(units / a.kv_heads / a.gtiles * a.q_heads),
                            dim3(D), 0, s, a);

@@ -104,6 +104,20 @@ def test_split_merge_over_several_weight_windows():
     assert max_err(split, oracle(args)) <= GATE[torch.float16]
 
 
+@pytest.mark.parametrize("batch,block_size,low,high", [(2, 256, 40000, 40001), (40, 16, 1500, 2600)])
+def test_streaming_loads_match_oracle(batch, block_size, low, high):
+    """Calls with more than 64 MiB of K/V within the tables' capacity load
+    rows with the non-temporal hint: split-K for two long sequences,
+    whole-sequence work-groups for forty ragged ones."""
+    gen = torch.Generator().manual_seed(batch)
+    lengths = tuple(torch.randint(low, high, (batch,), generator=gen).tolist())
+    args = decode_inputs(torch.float16, lengths=lengths, block_size=block_size, seed=batch)
+    width = args[3].shape[1]
+    assert batch * width * block_size * 8 * 128 * 4 > 64 << 20
+    actual = paged_attention(*to_dev(args), backend="hip")
+    assert max_err(actual, oracle(args)) <= GATE[torch.float16]
+
+
 def test_hip_rejects_bad_metadata_and_noncontiguous_query():
     args = to_dev(decode_inputs(torch.float16))
     args[4][0] = 0
