@@ -495,7 +495,9 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     }
     p.partition = (int)part;
     p.max_parts = (int)((cap + part - 1) / part);
-    p.stream = batch * cap * kv_heads * head_dim * 4 > kStreamBytes;
+    // In floating point: the size query runs before any shape check, where the
+    // integer product could overflow.
+    p.stream = (double)batch * (double)cap * (double)kv_heads * (double)head_dim * 4.0 > (double)kStreamBytes;
     return p;
 }
 
