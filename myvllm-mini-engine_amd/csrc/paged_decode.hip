@@ -361,16 +361,23 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
 // Split-K combine: out = sum_p acc_p 2^(m_p - M) / sum_p l_p 2^(m_p - M).
 // Partitions that never saw a valid token carry m = -inf and contribute 0;
 // an all-empty sequence produces 0.
-// One work-group of D threads per (sequence, query head); thread t owns
-// output dim t.  Every step loads many partitions at once: the
+// One work-group of whole waves per (sequence, query head), D rounded up to
+// 64 threads; thread t < D owns output dim t.  Threads past D take part in
+// the partition-maximum and weight loops and feed the identities (-inf for
+// the maximum, 0 for the sums) into the reductions, so a wave never reads a
+// lane that does not exist.  Every step loads many partitions at once: the
 // partition maxima one per thread, then (per window of partitions) the
 // weights 2^(m_p - ref) into LDS and each dim's partials eight at a time.
 constexpr int kMergeWindow = 2048;  // partition weights held in LDS at once
 
+template <int D>
+constexpr int merge_threads() { return (D + kWave - 1) / kWave * kWave; }
+
 template <typename T, int D>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
     static_assert(D <= 256, "one thread per output dim");
-    __shared__ float sm_red[256 / kWave];
+    constexpr int kThreads = merge_threads<D>();
+    __shared__ float sm_red[kThreads / kWave];
     __shared__ float sm_w[kMergeWindow];
     const int64_t bh = blockIdx.x;
     const int b = (int)(bh / a.q_heads);
@@ -381,7 +388,8 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
     const float* acc = a.ws_acc + bh * a.max_parts * D;
     const int tid = threadIdx.x;
     const int lane = tid & (kWave - 1), wave = tid / kWave;
-    constexpr int kWaves = (D + kWave - 1) / kWave;
+    constexpr int kWaves = kThreads / kWave;
+    const bool owns_dim = tid < D;
     auto block_reduce = [&](float v, bool is_max) __attribute__((always_inline)) {
 #pragma unroll
         for (int off = kWave / 2; off > 0; off >>= 1) {
@@ -397,7 +405,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
         return v;
     };
     float mx = kNegInf;
-    for (int p = tid; p < nparts; p += D) mx = fmaxf(mx, ml[2 * p]);
+    for (int p = tid; p < nparts; p += kThreads) mx = fmaxf(mx, ml[2 * p]);
     mx = block_reduce(mx, true);
     const float ref = mx == kNegInf ? 0.f : mx;
     constexpr int kBatch = 8;
@@ -405,12 +413,13 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
     for (int w0 = 0; w0 < nparts; w0 += kMergeWindow) {
         const int n = min(kMergeWindow, nparts - w0);
         __syncthreads();  // the previous window's weights are no longer read
-        for (int p = tid; p < n; p += D) {
+        for (int p = tid; p < n; p += kThreads) {
             const float w = fast_exp2(ml[2 * (w0 + p)] - ref);
             sm_w[p] = w;
             sum += ml[2 * (w0 + p) + 1] * w;
         }
         __syncthreads();
+        if (!owns_dim) continue;
         const float* accw = acc + (int64_t)w0 * D + tid;
         for (int p0 = 0; p0 < n; p0 += kBatch) {
             // Indices past the window's last partition re-read it; the
@@ -427,7 +436,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
         }
     }
     sum = block_reduce(sum, false);
-    static_cast<uint16_t*>(a.out)[bh * D + tid] = T::from_float(sum > 0.f ? o / sum : 0.f);
+    if (owns_dim) static_cast<uint16_t*>(a.out)[bh * D + tid] = T::from_float(sum > 0.f ? o / sum : 0.f);
 }
 
 struct DecodePlan {
@@ -525,7 +534,7 @@ void launch_decode(const DecodeArgs& a, const DecodePlan& p, int units, bool pag
     else launch_decode_nw<T, D, G, kSplitWaves>(a, units, page_uniform, p.stream, s);
     if (a.max_parts > 1)
         hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(units / a.kv_heads / a.gtiles * a.q_heads),
-                           dim3(D), 0, s, a);
+                           dim3(merge_threads<D>()), 0, s, a);
 }
 
 template <typename T, int D>

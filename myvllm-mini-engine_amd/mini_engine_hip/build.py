@@ -38,6 +38,10 @@ def library_path() -> Path:
     return LIB_DIR / LIB_NAME
 
 
+def digest_path() -> Path:
+    return LIB_DIR / "SOURCE_DIGEST"
+
+
 def sources() -> list[Path]:
     return sorted(SOURCE_DIR.glob("*.hip"))
 
@@ -71,8 +75,8 @@ def build_library(*, jobs: int | None = None, verbose: bool = False) -> Path:
     """Compile every csrc/*.hip for gfx950 and link libmvme_paged.so.
 
     Always recompiles (the build check must exercise the compiler).  The
-    source digest is written next to the library so loaders can detect a
-    stale build.
+    source digest is written next to the library; the loader refuses a
+    library whose digest differs from the current sources.
     """
     hipcc = _hipcc()
     build_dir = PACKAGE_DIR / "_build"
@@ -93,7 +97,7 @@ def build_library(*, jobs: int | None = None, verbose: bool = False) -> Path:
     tmp = target.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)])
     os.replace(tmp, target)
-    (LIB_DIR / "SOURCE_DIGEST").write_text(source_digest() + "\n")
+    digest_path().write_text(source_digest() + "\n")
     return target
 
 

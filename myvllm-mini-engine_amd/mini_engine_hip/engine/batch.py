@@ -1,7 +1,9 @@
 """Packed prefill metadata: the tensors the KV scatter and paged prefill read.
 
-Restates the contract of the reference's ``PrefillBatch.from_sequences``
-(mini_engine/engine/batch.py:66-137):
+Keeps the contract of the reference's ``PrefillBatch.from_sequences``
+(mini_engine/engine/batch.py:66-137) — the same fields, rules and error
+messages — but derives everything with whole-batch tensor operations on the
+host instead of walking positions one by one:
 
 * request r's queries sit at absolute positions start_r .. start_r+len_r-1;
 * slot = table[pos // block_size] * block_size + pos % block_size;
@@ -10,8 +12,14 @@ Restates the contract of the reference's ``PrefillBatch.from_sequences``
 * no slot is written twice, and no page written by one request may appear in
   another request's table (shared prefix pages are read-only).
 
-All validation happens on host values before any device tensor is built, so
-the scatter/prefill kernels can run with ``validate=False``.
+The checks run in three stages — argument types, the per-request layout
+(each rule over the whole batch at once), then the rules that relate
+requests (duplicate slots, written pages that another request reads) — and
+all of them finish before any device tensor exists, so the scatter and
+prefill kernels can run with ``validate=False``.  With several faults in one
+batch the first failing stage names the error (the reference reports the
+first faulty request instead); each single fault raises the reference's
+message.
 """
 
 from __future__ import annotations
@@ -21,24 +29,71 @@ from numbers import Integral
 
 import torch
 
-_INT64_MIN, _INT64_LIMIT = -(1 << 63), 1 << 63
+_INT64 = (-(1 << 63), (1 << 63) - 1)
 
 
-def _int_tuple(values, name):
+def _ints(values, name) -> list[int]:
+    """Plain Python ints from a list/tuple or a 1D int64 tensor."""
     if isinstance(values, torch.Tensor):
         if values.ndim != 1 or values.dtype != torch.int64:
             raise ValueError(f"{name} must be a 1D int64 tensor")
-        values = values.detach().cpu().tolist()
+        return values.detach().cpu().tolist()
     try:
-        items = tuple(values)
+        items = list(values)
     except TypeError as error:
         raise ValueError(f"{name} must be a sequence of integers") from error
-    for item in items:
-        if isinstance(item, bool) or not isinstance(item, Integral):
-            raise ValueError(f"{name} must contain integers")
-        if not _INT64_MIN <= item < _INT64_LIMIT:
-            raise ValueError(f"{name} values must fit int64")
-    return tuple(int(item) for item in items)
+    if not all(isinstance(v, Integral) and not isinstance(v, bool) for v in items):
+        raise ValueError(f"{name} must contain integers")
+    if items and not (_INT64[0] <= min(items) and max(items) <= _INT64[1]):
+        raise ValueError(f"{name} values must fit int64")
+    return [int(v) for v in items]
+
+
+def _positive(value, name) -> int:
+    if isinstance(value, bool) or not isinstance(value, Integral) or value <= 0:
+        raise ValueError(f"{name} must be a positive integer")
+    return int(value)
+
+
+def _padded_tables(rows) -> torch.Tensor:
+    """[B, widest] int64, short rows filled with -1 (the padding marker)."""
+    widest = max(len(row) for row in rows)
+    table = torch.full((len(rows), max(widest, 1)), -1, dtype=torch.int64)
+    for r, row in enumerate(rows):
+        if row:
+            table[r, :len(row)] = torch.tensor(row, dtype=torch.int64)
+    return table
+
+
+def _table_pages(table: torch.Tensor, num_blocks: int) -> torch.Tensor:
+    """Validate the page part of every table; return each row's page count."""
+    pad = table == -1
+    # Once a row is padded it must stay padded.
+    if bool((pad.cummax(dim=1).values & ~pad).any()):
+        raise ValueError("block table padding -1 must be trailing")
+    if bool((~pad & ((table < 0) | (table >= num_blocks))).any()):
+        raise ValueError("physical block ID out of range")
+    ordered = table.sort(dim=1).values
+    if bool(((ordered[:, 1:] == ordered[:, :-1]) & (ordered[:, 1:] != -1)).any()):
+        raise ValueError("a request block table cannot contain duplicate physical pages")
+    return (~pad).sum(dim=1)
+
+
+def _check_shared_writes(table: torch.Tensor, pages_per_row: torch.Tensor, slots: torch.Tensor,
+                         block_size: int) -> None:
+    """A page that receives new rows may be listed by one request only."""
+    rows = torch.arange(table.shape[0]).repeat_interleave(pages_per_row)
+    listed = table[table != -1]  # row-major, so it lines up with `rows`
+    written = torch.unique(slots // block_size)
+    hit = torch.isin(listed, written)
+    if not bool(hit.any()):
+        return
+    # Distinct (page, request) pairs among the written pages; a page with more
+    # than one is written by one request and read (or written) by another.
+    pairs = torch.unique(listed[hit] * table.shape[0] + rows[hit])
+    _, per_page = torch.unique(pairs // table.shape[0], return_counts=True)
+    if bool((per_page > 1).any()):
+        raise ValueError("prefill cannot write a physical page shared by requests")
 
 
 @dataclass(frozen=True)
@@ -66,76 +121,54 @@ class PrefillBatch:
         return self.query_offsets[-1]
 
     @classmethod
-    def from_sequences(cls, token_sequences, block_tables, query_starts, *,
-                       block_size, num_blocks, device):
-        for name, value in (("block_size", block_size), ("num_blocks", num_blocks)):
-            if isinstance(value, bool) or not isinstance(value, Integral) or value <= 0:
-                raise ValueError(f"{name} must be a positive integer")
-        block_size, num_blocks = int(block_size), int(num_blocks)
+    def from_sequences(cls, token_sequences, block_tables, query_starts, *, block_size, num_blocks, device):
+        block_size = _positive(block_size, "block_size")
+        num_blocks = _positive(num_blocks, "num_blocks")
+        # Stage 1: argument types.
         try:
-            sequences = [_int_tuple(seq, "token sequence") for seq in token_sequences]
+            sequences = [_ints(seq, "token sequence") for seq in token_sequences]
         except TypeError as error:
             raise ValueError("token_sequences must contain query sequences") from error
-        if not sequences or any(len(seq) == 0 for seq in sequences):
+        if not sequences or not all(sequences):
             raise ValueError("prefill batch requires nonempty query sequences")
-        starts = _int_tuple(query_starts, "query_starts")
+        starts = _ints(query_starts, "query_starts")
         if isinstance(block_tables, torch.Tensor):
             if block_tables.ndim != 2 or block_tables.dtype != torch.int64:
                 raise ValueError("block_tables must be a 2D int64 tensor")
             block_tables = block_tables.detach().cpu().tolist()
-        tables = [_int_tuple(row, "block table") for row in block_tables]
-        if not len(starts) == len(tables) == len(sequences):
+        rows = [_ints(row, "block table") for row in block_tables]
+        if not len(sequences) == len(starts) == len(rows):
             raise ValueError("queries, query_starts and block_tables must have equal batch size")
 
-        ids, positions, slots, contexts, offsets, clean = [], [], [], [], [0], []
-        written = set()
-        readers: dict[int, set] = {}
-        writers: dict[int, set] = {}
-        for request, (tokens, table, start) in enumerate(zip(sequences, tables, starts)):
-            if start < 0:
-                raise ValueError("query_starts must be nonnegative")
-            if min(tokens) < 0:
-                raise ValueError("token IDs must be nonnegative")
-            active = len(table)
-            for index, page in enumerate(table):
-                if page == -1:
-                    active = index
-                    break
-            if any(page != -1 for page in table[active:]):
-                raise ValueError("block table padding -1 must be trailing")
-            table = table[:active]
-            if any(not 0 <= page < num_blocks for page in table):
-                raise ValueError("physical block ID out of range")
-            if len(set(table)) != len(table):
-                raise ValueError("a request block table cannot contain duplicate physical pages")
-            end = start + len(tokens)
-            if end > len(table) * block_size:
-                raise ValueError("query range exceeds supplied block table capacity")
-            for page in table:
-                readers.setdefault(page, set()).add(request)
-            for pos in range(start, end):
-                page = table[pos // block_size]
-                slot = page * block_size + pos % block_size
-                if slot in written:
-                    raise ValueError("prefill batch contains duplicate writable KV slots")
-                written.add(slot)
-                writers.setdefault(page, set()).add(request)
-                positions.append(pos)
-                slots.append(slot)
-            ids.extend(tokens)
-            contexts.append(end)
-            offsets.append(offsets[-1] + len(tokens))
-            clean.append(table)
-        for page, who in writers.items():
-            if len(readers[page] | who) > 1:
-                raise ValueError("prefill cannot write a physical page shared by requests")
+        # Stage 2: each request's own layout, checked for all requests at once.
+        lengths = torch.tensor([len(seq) for seq in sequences], dtype=torch.int64)
+        start = torch.tensor(starts, dtype=torch.int64)
+        token_ids = torch.tensor([t for seq in sequences for t in seq], dtype=torch.int64)
+        if bool((start < 0).any()):
+            raise ValueError("query_starts must be nonnegative")
+        if bool((token_ids < 0).any()):
+            raise ValueError("token IDs must be nonnegative")
+        table = _padded_tables(rows)
+        pages_per_row = _table_pages(table, num_blocks)
+        ends = start + lengths
+        if bool((ends > pages_per_row * block_size).any()):
+            raise ValueError("query range exceeds supplied block table capacity")
 
-        width = max(len(table) for table in clean)
-        padded = [list(table) + [-1] * (width - len(table)) for table in clean]
+        # Positions and slots of every packed token.
+        owner = torch.arange(len(sequences)).repeat_interleave(lengths)
+        offsets = torch.cat([torch.zeros(1, dtype=torch.int64), lengths.cumsum(0)])
+        positions = start[owner] + torch.arange(token_ids.numel()) - offsets[owner]
+        pages = table[owner, positions // block_size]
+        slots = pages * block_size + positions % block_size
 
-        def tensor(values):
-            return torch.tensor(values, dtype=torch.int64, device=device)
+        # Stage 3: rules between requests.
+        if torch.unique(slots).numel() != slots.numel():
+            raise ValueError("prefill batch contains duplicate writable KV slots")
+        _check_shared_writes(table, pages_per_row, slots, block_size)
 
-        return cls(tensor(ids), tensor(positions), tensor(slots), tensor(offsets), tensor(list(starts)),
-                   tensor(contexts), tensor(padded), tuple(len(seq) for seq in sequences), tuple(offsets),
-                   starts, tuple(clean), block_size, num_blocks)
+        width = int(pages_per_row.max())
+        clean = tuple(tuple(row[:int(n)]) for row, n in zip(rows, pages_per_row))
+        on_device = [t.to(device) for t in (token_ids, positions, slots, offsets, start, ends,
+                                           table[:, :width].contiguous())]
+        return cls(*on_device, tuple(lengths.tolist()), tuple(offsets.tolist()), tuple(starts), clean,
+                   block_size, num_blocks)

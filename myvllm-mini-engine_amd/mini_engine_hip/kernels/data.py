@@ -93,23 +93,34 @@ def write_kv_cache_batch(key_cache, value_cache, block_tables, token_offsets, ke
 
 
 def _row_stride(tensor):
-    """Token stride (elements) if the [heads, dim] part of each row is dense."""
-    if tensor.shape[0] <= 1:
-        return tensor.shape[1] * tensor.shape[2], tensor
-    if tensor.stride(2) == 1 and tensor.stride(1) == tensor.shape[2] and tensor.stride(0) >= tensor.shape[1] * tensor.shape[2]:
+    """(token stride in elements, tensor) for a kernel that reads [T, H, D] rows.
+
+    The kernels read each token's [heads, head_dim] block as one dense run
+    of H*D elements starting at ``t * stride``.  A view whose rows are dense
+    (a slice of a fused QKV projection) is passed as it is, with its token
+    stride; any other layout — for one token as for many — is copied to a
+    contiguous tensor first.  Strides of dimensions of size 1 never matter.
+    """
+    tokens, heads, dim = tensor.shape
+    dense_rows = (dim == 1 or tensor.stride(2) == 1) and (heads == 1 or tensor.stride(1) == dim)
+    if dense_rows and tokens <= 1:
+        return heads * dim, tensor
+    if dense_rows and tensor.stride(0) >= heads * dim:
         return tensor.stride(0), tensor
     tensor = tensor.contiguous()
-    return tensor.shape[1] * tensor.shape[2], tensor
+    return heads * dim, tensor
 
 
 def write_kv_cache_slots(key_cache, value_cache, slot_mapping, key, value,
                          *, backend="hip", validate=True):
-    """Scatter packed KV rows to unique physical ``page * block_size + offset`` slots.
+    """Copy row t of ``key``/``value`` to cache slot ``slot_mapping[t]``.
 
-    ``validate=False`` trusts slot contents checked by the batch factory;
-    shape, dtype, device and cache layout checks remain active without a
-    device sync.  ``key``/``value`` may be strided views (e.g. slices of a
-    fused QKV projection) as long as each [kv_heads, head_dim] row is dense.
+    A slot numbers a token row of the whole pool, ``page * block_size +
+    offset``.  With ``validate=True`` the slots are read on the host and must
+    be in range and distinct, and no source may alias a cache; with
+    ``validate=False`` (graph capture) only shapes, dtypes and devices are
+    checked, and the kernel skips any slot outside the pool.  The sources
+    may be strided views whose per-token [kv_heads, head_dim] rows are dense.
     """
     _backend(backend)
     if (key_cache.ndim != 4 or value_cache.shape != key_cache.shape

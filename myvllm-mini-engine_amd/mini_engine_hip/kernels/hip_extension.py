@@ -80,12 +80,33 @@ class HipLibrary:
         return int(self._lib.mvme_greedy_argmax_workspace_size(*args))
 
 
+def check_build_digest(digest_file, expected: str) -> None:
+    """Refuse a library built from other sources than the ones beside it.
+
+    ``build_library`` writes the sha256 of the HIP sources and headers next to
+    the library; a missing or different digest means the library is stale.
+    """
+    try:
+        recorded = digest_file.read_text().strip()
+    except OSError as error:
+        raise RuntimeError(f"no build digest at {digest_file}: rebuild the HIP library "
+                           f"(python -m mini_engine_hip.build)") from error
+    if recorded != expected:
+        raise RuntimeError(f"stale HIP library: the sources changed since it was built "
+                           f"(digest {recorded[:12]} != {expected[:12]}); rebuild with "
+                           f"python -m mini_engine_hip.build")
+
+
 @functools.lru_cache(maxsize=1)
 def load_hip_extension() -> HipLibrary:
-    """Load the prebuilt library; build it first only if no build exists."""
+    """Load the prebuilt library; build it first only if no build exists.
+
+    An existing library must carry the digest of the current sources.
+    """
     path = _build.library_path()
     if not path.exists():
         _build.build_library()
+    check_build_digest(_build.digest_path(), _build.source_digest())
     try:
         lib = ctypes.CDLL(str(path))
     except OSError as error:

@@ -32,9 +32,14 @@ def linear_rows(x, weight, bias=None, *, out=None):
         raise ValueError("HIP linear rows needs row-major input and a contiguous weight")
     if bias is not None and (bias.shape != (weight.shape[0],) or bias.dtype != x.dtype or not bias.is_contiguous()):
         raise ValueError("bias must be a contiguous [out_features] tensor of the input dtype")
+    if weight.device != x.device or (bias is not None and bias.device != x.device):
+        raise ValueError("input, weight and bias must share a device")
     rows, out_features = x.shape[0], weight.shape[0]
     if out is None:
         out = torch.empty(rows, out_features, dtype=x.dtype, device=x.device)
+    elif (out.shape != (rows, out_features) or out.dtype != x.dtype or not out.is_contiguous()
+          or out.device != x.device):
+        raise ValueError("out must be a contiguous [rows, out_features] tensor of the input dtype and device")
     lib = ext.load_hip_extension()
     with torch.cuda.device(x.device):
         lib.call("mvme_linear_rows", out.data_ptr(), x.data_ptr(), weight.data_ptr(),

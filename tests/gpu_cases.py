@@ -32,3 +32,20 @@ def prefill_inputs(dtype, *, head_dim=16, seed=631):
     q = torch.randn(8, 4, head_dim, generator=gen).to(dtype)
     meta = [torch.tensor(x, dtype=torch.int64) for x in ([0, 3, 8], [5, 1], [[5, 1, -1], [2, 7, -1]], [8, 6])]
     return (q, key, value, *meta)
+
+
+ROPE_ATOL = {torch.float16: 0.001, torch.bfloat16: 0.004}
+ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
+
+
+def assert_rope_close(actual, expected, normed, dtype):
+    """Reference tolerance, or two ulps of the rotated pair, per element; >= 99% bit-exact."""
+    actual, expected, normed = actual.cpu().float(), expected.float(), normed.float()
+    half = normed.shape[-1] // 2
+    pair = normed[..., :half].abs() + normed[..., half:].abs()
+    bound = 2 * ULP[dtype] * torch.cat((pair, pair), -1) + 1e-6
+    diff = (actual - expected).abs()
+    reference_ok = diff <= ROPE_ATOL[dtype] + 0.01 * expected.abs()
+    assert bool((reference_ok | (diff <= bound)).all()), f"max diff {diff.max().item()}"
+    exact = (actual == expected).float().mean().item()
+    assert exact >= 0.99, f"only {exact:.4f} of the elements are bit-identical"

@@ -115,6 +115,34 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
         ext.load_hip_extension.cache_clear()
 
 
+def test_stale_library_is_refused(tmp_path):
+    """A library whose recorded source digest differs from the sources beside it
+    (or that has none) is refused before it is loaded."""
+    current = hip_build.source_digest()
+    digest = tmp_path / "SOURCE_DIGEST"
+    with pytest.raises(RuntimeError, match="no build digest"):
+        ext.check_build_digest(digest, current)
+    digest.write_text("0" * 64 + "\n")
+    with pytest.raises(RuntimeError, match="stale HIP library"):
+        ext.check_build_digest(digest, current)
+    digest.write_text(current + "\n")
+    ext.check_build_digest(digest, current)
+    # The in-tree build carries the digest of the current sources.
+    assert hip_build.digest_path().read_text().strip() == current
+
+
+def test_loader_checks_the_digest(monkeypatch, tmp_path):
+    ext.load_hip_extension.cache_clear()
+    planted = tmp_path / "SOURCE_DIGEST"
+    planted.write_text("f" * 64)
+    monkeypatch.setattr(hip_build, "digest_path", lambda: planted)
+    try:
+        with pytest.raises(RuntimeError, match="stale HIP library"):
+            ext.load_hip_extension()
+    finally:
+        ext.load_hip_extension.cache_clear()
+
+
 def test_argmax_workspace_plan(lib):
     # Enough slices per row to cover the CUs twice (>= 2048 elements each), a single slice otherwise.
     assert lib.argmax_workspace_size(32, 151936) == 32 * 16 * 8

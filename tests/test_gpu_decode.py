@@ -228,3 +228,48 @@ def test_c4_ragged_shared_prefix_bf16():
     # Shared prefix pages really are shared: 16 tables name the same first 64 pages.
     tables = case["block_tables"].cpu()
     assert all(torch.equal(tables[i, :64], tables[0, :64]) for i in range(16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim", [16, 32, 80, 96, 128])
+@pytest.mark.parametrize("partition", [64, 0])
+def test_split_merge_with_strongly_negative_scores(dtype, dim, partition):
+    """Every score far below -126 in log2 units (q = -c * |k|): the merge's
+    reference maximum is negative, so a reduction that let absent lanes
+    contribute 0 would underflow every partition weight and return zeros.
+    Head dims below 64 or not a multiple of 64 run the merge in a partial wave."""
+    q, k, v, t, l, bs = decode_inputs(dtype, head_dim=dim, lengths=(300, 1000, 2500), block_size=16, seed=dim)
+    k = k.abs()
+    q = torch.full_like(q, -256.0)
+    args = (q, k, v, t, l, bs)
+    # The largest score of the whole cache, in log2 units, is far below -126.
+    assert -256.0 * k.float().sum(-1).min().item() / dim ** 0.5 * 1.4427 < -300
+    print(f"negative-score merge {dtype} D={dim} partition={partition}", flush=True)
+    actual = paged_attention(*to_dev(args), backend="hip", partition_tokens=partition)
+    expected = oracle(args)
+    assert actual.float().abs().amax().item() > 0.1
+    assert max_err(actual, expected) <= GATE[dtype]
+
+
+def test_c2_decode_b8_with_scatter_bf16():
+    """The B8 / ctx 512 / block 16 / 2048-page workload exactly: the new token
+    of each sequence is scattered to position 511 (slot table[b, 31]*16+15),
+    rows bit-exact, then decode over the updated pages against the oracle."""
+    from mini_engine_hip.kernels.data import write_kv_cache_slots
+    from mini_engine_hip.workloads import decode_b8_with_scatter
+
+    case = decode_b8_with_scatter(device=DEV)
+    kc, vc = case["key_cache"], case["value_cache"]
+    assert kc.shape == (2048, 16, 8, 128) and kc.dtype == torch.bfloat16
+    want_k, want_v = kc.cpu(), vc.cpu()
+    paged_oracle.write_kv_cache_slots(want_k, want_v, case["slot_mapping"].cpu(), case["new_key"].cpu(),
+                                      case["new_value"].cpu())
+    write_kv_cache_slots(kc, vc, case["slot_mapping"], case["new_key"], case["new_value"], backend="hip")
+    torch.cuda.synchronize()
+    assert torch.equal(kc.cpu(), want_k) and torch.equal(vc.cpu(), want_v)
+    assert case["context_lens"].tolist() == [512] * 8
+    args = [case["query"], kc, vc, case["block_tables"], case["context_lens"], 16]
+    actual = paged_attention(*args, backend="hip")
+    expected = oracle([a.cpu() if isinstance(a, torch.Tensor) else a for a in args])
+    assert max_err(actual, expected) <= GATE[torch.bfloat16]
+    torch.testing.assert_close(actual.float().cpu(), expected, atol=0.004, rtol=0.015)

@@ -80,3 +80,14 @@ def test_linear_rows_rejects_unsupported_shapes():
     with pytest.raises(RuntimeError, match="multiple of 16"):
         linear_rows(torch.randn(4, 64, device=DEV, dtype=torch.bfloat16),
                     torch.randn(24, 64, device=DEV, dtype=torch.bfloat16))
+    # A caller-supplied output must match the product exactly.
+    x = torch.randn(4, 64, device=DEV, dtype=torch.bfloat16)
+    w = torch.randn(16, 64, device=DEV, dtype=torch.bfloat16)
+    for bad in (torch.empty(4, 8, device=DEV, dtype=torch.bfloat16),
+                torch.empty(4, 16, device=DEV, dtype=torch.float16),
+                torch.empty(16, 4, device=DEV, dtype=torch.bfloat16).t(),
+                torch.empty(4, 16, dtype=torch.bfloat16)):
+        with pytest.raises(ValueError, match="out must be"):
+            linear_rows(x, w, out=bad)
+    with pytest.raises(ValueError, match="share a device"):
+        linear_rows(x, w, torch.zeros(16, dtype=torch.bfloat16))

@@ -18,13 +18,12 @@ oracle (a dropped rounding step changes far more than 1%).
 import pytest
 import torch
 
+from gpu_cases import assert_rope_close
 from mini_engine_hip.kernels.rope import qk_norm_rope_write_kv
 from oracle import paged_oracle
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-ROPE_ATOL = {torch.float16: 0.001, torch.bfloat16: 0.004}
-ULP = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
 
 
 def fused_case(dtype, tokens, heads, kv_heads, dim, block, pages, seed, pad=0):
@@ -46,19 +45,6 @@ def split_qkv(qkv, heads, kv_heads, dim):
     k = qkv[:, off + heads * dim:off + (heads + kv_heads) * dim].view(t, kv_heads, dim)
     v = qkv[:, off + (heads + kv_heads) * dim:].view(t, kv_heads, dim)
     return q, k, v
-
-
-def assert_rope_close(actual, expected, normed, dtype):
-    """Reference tolerance, or two ulps of the rotated pair, per element; >= 99% bit-exact."""
-    actual, expected, normed = actual.cpu().float(), expected.float(), normed.float()
-    half = normed.shape[-1] // 2
-    pair = normed[..., :half].abs() + normed[..., half:].abs()
-    bound = 2 * ULP[dtype] * torch.cat((pair, pair), -1) + 1e-6
-    diff = (actual - expected).abs()
-    reference_ok = diff <= ROPE_ATOL[dtype] + 0.01 * expected.abs()
-    assert bool((reference_ok | (diff <= bound)).all()), f"max diff {diff.max().item()}"
-    exact = (actual == expected).float().mean().item()
-    assert exact >= 0.99, f"only {exact:.4f} of the elements are bit-identical"
 
 
 def run_and_check(dtype, tokens, heads, kv_heads, dim, block, pages, seed, *, slots=None, tables=None,
@@ -170,3 +156,36 @@ def test_repeated_calls_are_bit_identical_and_validation_raises():
     empty = qk_norm_rope_write_kv(q[:0], k[:0], v[:0], wq, wk, cos[:0], sin[:0], kc, vc,
                                   slot_mapping=slots[:0])
     assert empty.shape == (0, heads, dim)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_single_token_transposed_sources(dtype):
+    """Decode batch of one whose q/k/v are transposed views ([1, H, D] with
+    non-dense rows): the wrapper copies them, so the results equal those of
+    the contiguous tensors."""
+    heads, kv_heads, dim, block, pages = 4, 2, 64, 16, 3
+    qkv, cos, sin, wq, wk, kc, vc = fused_case(dtype, 1, heads, kv_heads, dim, block, pages, seed=31)
+    q, k, v = split_qkv(qkv, heads, kv_heads, dim)
+    tables = torch.tensor([[2, 0]], dtype=torch.int64)
+    positions = torch.tensor([19], dtype=torch.int64)
+    ke, ve = kc.clone(), vc.clone()
+    expected_q = paged_oracle.qk_norm_rope_write_kv(q, k, v, wq, wk, cos, sin, ke, ve, block_tables=tables,
+                                                    positions=positions)
+
+    def transposed(x):  # same values, stored [1, D, H] and viewed as [1, H, D]
+        return x.to(DEV).transpose(1, 2).contiguous().transpose(1, 2)
+
+    dq, dk, dv = transposed(q), transposed(k), transposed(v)
+    assert not (dq.is_contiguous() or dk.is_contiguous() or dv.is_contiguous())
+    kd, vd = kc.to(DEV), vc.to(DEV)
+    got_q = qk_norm_rope_write_kv(dq, dk, dv, wq.to(DEV), wk.to(DEV), cos.to(DEV), sin.to(DEV), kd, vd,
+                                  block_tables=tables.to(DEV), positions=positions.to(DEV))
+    ref_q = qk_norm_rope_write_kv(q.to(DEV).contiguous(), k.to(DEV).contiguous(), v.to(DEV).contiguous(),
+                                  wq.to(DEV), wk.to(DEV), cos.to(DEV), sin.to(DEV), kc.to(DEV), vc.to(DEV),
+                                  block_tables=tables.to(DEV), positions=positions.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(got_q, ref_q)
+    assert_rope_close(got_q, expected_q, paged_oracle.rms_norm(q, wq), dtype)
+    assert torch.equal(vd.cpu(), ve)
+    written = ~(ke == kc).all(-1).all(-1)
+    assert torch.equal(kd.cpu()[~written], ke[~written])

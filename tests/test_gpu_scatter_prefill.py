@@ -70,6 +70,27 @@ def test_slot_scatter_strided_sources_and_untouched_rows():
     assert torch.equal(dk.cpu(), want_k) and torch.equal(dv.cpu(), want_v)
 
 
+@pytest.mark.parametrize("tokens", [1, 2])
+def test_slot_scatter_transposed_sources_one_token(tokens):
+    """A source whose [kv_heads, head_dim] rows are not dense (a transposed
+    view) is copied before the kernel reads it, also for a single token."""
+    dtype = torch.float16
+    gen = torch.Generator().manual_seed(5 + tokens)
+    cache_k = torch.randn(4, 16, 8, 64, generator=gen).to(dtype)
+    cache_v = torch.randn(4, 16, 8, 64, generator=gen).to(dtype)
+    raw_k = torch.randn(tokens, 64, 8, generator=gen).to(dtype)
+    raw_v = torch.randn(tokens, 64, 8, generator=gen).to(dtype)
+    slots = torch.tensor([37, 5][:tokens], dtype=torch.int64)
+    want_k, want_v = cache_k.clone(), cache_v.clone()
+    paged_oracle.write_kv_cache_slots(want_k, want_v, slots, raw_k.transpose(1, 2), raw_v.transpose(1, 2))
+    dk, dv = cache_k.to(DEV), cache_v.to(DEV)
+    src_k, src_v = raw_k.to(DEV).transpose(1, 2), raw_v.to(DEV).transpose(1, 2)
+    assert not src_k.is_contiguous()
+    write_kv_cache_slots(dk, dv, slots.to(DEV), src_k, src_v, backend="hip")
+    torch.cuda.synchronize()
+    assert torch.equal(dk.cpu(), want_k) and torch.equal(dv.cpu(), want_v)
+
+
 def test_slot_scatter_trusted_out_of_range_slots_are_skipped():
     dtype = torch.float16
     cache_k = torch.zeros(4, 4, 2, 16, dtype=dtype, device=DEV)

@@ -142,6 +142,42 @@ def test_prefill_metadata_rejects_invalid_layout(sequences, tables, starts, erro
         metadata(sequences, tables, starts)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_prefill_metadata_matches_oracle_on_random_batches(seed):
+    """Ragged batches whose requests share read-only prefix pages: every field
+    equals the oracle's per-position restatement of the rules."""
+    gen = torch.Generator().manual_seed(seed)
+    bs, shared = 4, [40, 41]  # two prefix pages, read by every request
+    order = torch.randperm(32, generator=gen).tolist()
+    sequences, tables, starts = [], [], []
+    for r in range(int(torch.randint(1, 6, (1,), generator=gen))):
+        count = int(torch.randint(1, 9, (1,), generator=gen))
+        start = 8 + int(torch.randint(0, 5, (1,), generator=gen))  # past the shared 8 tokens
+        private = -(-(start + count) // bs) - 2
+        table = shared + order[:private]
+        order = order[private:]
+        tables.append(table + [-1] * int(torch.randint(0, 3, (1,), generator=gen)))
+        sequences.append(torch.randint(0, 1000, (count,), generator=gen).tolist())
+        starts.append(start)
+    batch = metadata(sequences, tables, starts, num_blocks=64)
+    ref = paged_oracle.prefill_metadata(sequences, tables, starts, bs)
+    assert batch.positions.tolist() == ref["positions"]
+    assert batch.slot_mapping.tolist() == ref["slot_mapping"]
+    assert batch.cu_seqlens_q.tolist() == ref["cu_seqlens_q"]
+    assert batch.context_lens.tolist() == ref["context_lens"]
+    assert batch.block_tables.tolist() == ref["block_tables"]
+    assert batch.input_ids.tolist() == [t for s in sequences for t in s]
+    assert batch.query_starts.tolist() == starts
+    # Writing into a shared page is refused once another request reads it.
+    starts_low = list(starts)
+    starts_low[-1] = 7
+    if len(starts) > 1:
+        with pytest.raises(ValueError, match="shared by requests"):
+            metadata(sequences, tables, starts_low, num_blocks=64)
+    else:
+        assert metadata(sequences, tables, starts_low, num_blocks=64).slot_mapping[0].item() == 41 * bs + 3
+
+
 def test_page_pool_shared_prefix_refcounts():
     """block_manager.py:55-105 semantics: a cached prefix attached to several requests."""
     pool = PagePool(12, 4, order=[5, 3, 11, 0, 1, 2, 4, 6, 7, 8, 9, 10])
@@ -203,3 +239,22 @@ def test_hip_linear_contract_on_cpu():
         HipLinear(7, 5)(x)
     with pytest.raises(ValueError, match="CUDA"):
         linear_rows(torch.randn(2, 64), torch.randn(16, 64))
+
+
+def test_row_stride_passes_only_dense_rows():
+    """The scatter and fused-RoPE kernels read each token's [heads, dim] block
+    as one dense run; any other view is copied first, also for one token."""
+    from mini_engine_hip.kernels.data import _row_stride
+
+    fused = torch.randn(5, 3 * 64).view(5, 3, 4, 16)[:, 1]  # one slice of a fused projection
+    stride, same = _row_stride(fused)
+    assert stride == 3 * 64 and same.data_ptr() == fused.data_ptr()
+    for tokens in (1, 3):
+        transposed = torch.randn(tokens, 64, 4).transpose(1, 2)  # [T, 4, 64], not dense per row
+        assert not transposed.is_contiguous()
+        stride, fixed = _row_stride(transposed)
+        assert stride == 4 * 64 and fixed.is_contiguous() and torch.equal(fixed, transposed)
+    one = torch.randn(1, 4, 16)
+    assert _row_stride(one) == (64, one)
+    single_head = torch.randn(6, 1, 16)[:, :, :]
+    assert _row_stride(single_head)[0] == 16
