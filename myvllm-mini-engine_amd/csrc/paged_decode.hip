@@ -559,6 +559,9 @@ void launch_decode_d(const DecodeArgs& a, int64_t head_dim, const DecodePlan& p,
     }
 }
 
+constexpr int64_t kMaxCapacity = 1048576;     // tokens a block table may address
+constexpr int64_t kMaxBatchHeads = 2147483647; // batch * q_heads
+
 int check_decode_shapes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                         int64_t num_blocks, int64_t block_size, int64_t table_width, int dtype) {
     if (!valid_dtype(dtype)) return fail(MVME_EINVAL, "FP16/BF16 required");
@@ -569,8 +572,10 @@ int check_decode_shapes(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_
     if (decode_tile_tokens(head_dim) == 0)
         return fail(MVME_EINVAL, "supported head_dim: 16,32,64,80,96,128,192,256");
     if (table_width <= 0) return fail(MVME_EINVAL, "invalid block table");
-    if (table_width * block_size > 1048576) return fail(MVME_EINVAL, "maximum table capacity is 1M tokens");
-    if (batch * q_heads > 2147483647) return fail(MVME_EINVAL, "batch/head product too large");
+    if (block_size > kMaxCapacity || table_width > kMaxCapacity || table_width * block_size > kMaxCapacity)
+        return fail(MVME_EINVAL, "maximum table capacity is 1M tokens");
+    if (batch > kMaxBatchHeads || q_heads > kMaxBatchHeads || batch * q_heads > kMaxBatchHeads)
+        return fail(MVME_EINVAL, "batch/head product too large");
     return MVME_OK;
 }
 
@@ -584,6 +589,11 @@ extern "C" size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_h
                                                       int64_t table_width, int64_t partition_tokens) {
     if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || block_size <= 0 ||
         table_width <= 0 || decode_tile_tokens(head_dim) == 0)
+        return 0;
+    // The limits mvme_paged_attention enforces; inside them every product of
+    // the plan fits its type.
+    if (block_size > kMaxCapacity || table_width > kMaxCapacity || table_width * block_size > kMaxCapacity ||
+        batch > kMaxBatchHeads || q_heads > kMaxBatchHeads || batch * q_heads > kMaxBatchHeads)
         return 0;
     const DecodePlan p = make_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, table_width,
                                           partition_tokens);

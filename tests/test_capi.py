@@ -48,6 +48,14 @@ def test_workspace_size_is_a_host_function(lib):
     size = lib.workspace_size(1, 16, 8, 128, 16, 256, 512)
     assert size == 1 * 16 * 8 * (128 + 2) * 4
     assert lib.workspace_size(1, 16, 8, 100, 16, 256, 0) == 0  # unsupported head dim
+    # Shapes the entry point refuses report no workspace instead of an
+    # overflowed size: capacity above 1M tokens, batch * heads above 2^31 - 1,
+    # and products that would overflow int64.
+    assert lib.workspace_size(1, 16, 8, 128, 16, 65537, 0) == 0
+    assert lib.workspace_size(1, 16, 8, 128, 1 << 62, 4, 0) == 0
+    assert lib.workspace_size(1 << 31, 2, 1, 128, 16, 256, 64) == 0
+    assert lib.workspace_size(1 << 40, 1 << 40, 1, 128, 16, 256, 64) == 0
+    assert lib.workspace_size(1, 16, 8, 128, 16, 65536, 64) == 16 * 16384 * 130 * 4
 
 
 def _status(lib, name, *args):
