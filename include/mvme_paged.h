@@ -147,6 +147,27 @@ int mvme_paged_attention(void* out, const void* query,
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * mvme_paged_attention without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments, kernels and results as mvme_paged_attention; the split-K
+ * partials go to a fixed 8 MiB scratch array that the library holds on each
+ * device until the process ends, so the call allocates nothing.  Calls whose
+ * plan needs more scratch than 8 MiB (mvme_paged_attention_workspace_size
+ * above 8388608) fail with MVME_EWORKSPACE before any launch.
+ * The first call on a device resolves the scratch address there (make it
+ * outside graph capture).  Every call on one device shares that device's
+ * scratch: calls that may overlap on one GPU (different streams without an
+ * ordering between them) race and must not be issued.
+ */
+int mvme_paged_attention_noalloc(void* out, const void* query,
+                                 const void* key_cache, const void* value_cache,
+                                 const int64_t* block_tables, const int64_t* context_lens,
+                                 int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                 int64_t num_blocks, int64_t block_size, int64_t table_width,
+                                 int64_t partition_tokens, int dtype, void* stream);
+
+/*
  * Bytes of device workspace mvme_paged_prefill_attention needs for these
  * shapes (0 when no query block is split over key chunks).  Pure host
  * function.  chunk_tokens: 0 selects the library's default key chunking.

@@ -21,6 +21,8 @@
 // the scale.  Each token group of lanes keeps its own running max/sum/acc;
 // groups, then waves (through LDS), are merged at the end.  Sequences that
 // fit one partition write the output directly from the attention kernel.
+#include <mutex>
+
 #include "mvme_common.h"
 
 namespace mvme {
@@ -601,24 +603,17 @@ extern "C" size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_h
     return (size_t)batch * q_heads * p.max_parts * (head_dim + 2) * sizeof(float);
 }
 
-extern "C" int mvme_paged_attention(void* out, const void* query, const void* key_cache,
-                                    const void* value_cache, const int64_t* block_tables,
-                                    const int64_t* context_lens, int64_t batch, int64_t q_heads,
-                                    int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
-                                    int64_t block_size, int64_t table_width, int64_t partition_tokens,
-                                    int dtype, void* workspace, size_t workspace_bytes, void* stream) {
-    if (int rc = check_decode_shapes(batch, q_heads, kv_heads, head_dim, num_blocks, block_size,
-                                     table_width, dtype))
-        return rc;
-    if (!out || !query || !key_cache || !value_cache || !block_tables || !context_lens)
-        return fail(MVME_EINVAL, "paged attention received a null pointer");
+namespace mvme {
+namespace {
+
+// Shapes checked, workspace sized: plan the call and launch its kernels.
+int launch_paged_attention(void* out, const void* query, const void* key_cache, const void* value_cache,
+                           const int64_t* block_tables, const int64_t* context_lens, int64_t batch,
+                           int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
+                           int64_t block_size, int64_t table_width, int64_t partition_tokens, int dtype,
+                           size_t need, void* workspace, void* stream) {
     const DecodePlan p = make_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, table_width,
                                           partition_tokens);
-    const size_t need = mvme_paged_attention_workspace_size(batch, q_heads, kv_heads, head_dim, block_size,
-                                                            table_width, partition_tokens);
-    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
-        return fail(MVME_EWORKSPACE, "paged attention workspace too small: need " + std::to_string(need) +
-                                         " bytes, got " + std::to_string(workspace_bytes));
     const int64_t group = q_heads / kv_heads;
     const int64_t units = batch * kv_heads * (group / p.gtile);
     if (units > 2147483647) return fail(MVME_EINVAL, "batch/head product too large");
@@ -651,4 +646,82 @@ extern "C" int mvme_paged_attention(void* out, const void* query, const void* ke
     if (dtype == MVME_FP16) launch_decode_d<Half>(a, head_dim, p, (int)units, page_uniform, s);
     else launch_decode_d<BFloat16>(a, head_dim, p, (int)units, page_uniform, s);
     return check_launch("paged attention");
+}
+
+// Split-K scratch of the allocation-free entry point: one array per device,
+// held until the process ends.  The kernels write every partial they later
+// read, so nothing in it needs clearing between calls.
+constexpr size_t kScratchBytes = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// Device address of `scratch` on each device, resolved on the first call made
+// with that device current (the host-side name is only a handle).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int device_scratch(void** ptr) {
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices)
+        return fail(MVME_ELAUNCH, "paged attention (no-alloc): no usable current HIP device");
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (g_scratch_ptr[device] == nullptr) {
+        void* address = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || address == nullptr)
+            return fail(MVME_ELAUNCH, std::string("paged attention (no-alloc): scratch address: ") +
+                                          hipGetErrorString(err));
+        g_scratch_ptr[device] = address;
+    }
+    *ptr = g_scratch_ptr[device];
+    return MVME_OK;
+}
+
+}  // namespace
+}  // namespace mvme
+
+extern "C" int mvme_paged_attention(void* out, const void* query, const void* key_cache,
+                                    const void* value_cache, const int64_t* block_tables,
+                                    const int64_t* context_lens, int64_t batch, int64_t q_heads,
+                                    int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
+                                    int64_t block_size, int64_t table_width, int64_t partition_tokens,
+                                    int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+    if (int rc = check_decode_shapes(batch, q_heads, kv_heads, head_dim, num_blocks, block_size,
+                                     table_width, dtype))
+        return rc;
+    if (!out || !query || !key_cache || !value_cache || !block_tables || !context_lens)
+        return fail(MVME_EINVAL, "paged attention received a null pointer");
+    const size_t need = mvme_paged_attention_workspace_size(batch, q_heads, kv_heads, head_dim, block_size,
+                                                            table_width, partition_tokens);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(MVME_EWORKSPACE, "paged attention workspace too small: need " + std::to_string(need) +
+                                         " bytes, got " + std::to_string(workspace_bytes));
+    return launch_paged_attention(out, query, key_cache, value_cache, block_tables, context_lens, batch,
+                                  q_heads, kv_heads, head_dim, num_blocks, block_size, table_width,
+                                  partition_tokens, dtype, need, workspace, stream);
+}
+
+extern "C" int mvme_paged_attention_noalloc(void* out, const void* query, const void* key_cache,
+                                            const void* value_cache, const int64_t* block_tables,
+                                            const int64_t* context_lens, int64_t batch, int64_t q_heads,
+                                            int64_t kv_heads, int64_t head_dim, int64_t num_blocks,
+                                            int64_t block_size, int64_t table_width, int64_t partition_tokens,
+                                            int dtype, void* stream) {
+    if (int rc = check_decode_shapes(batch, q_heads, kv_heads, head_dim, num_blocks, block_size,
+                                     table_width, dtype))
+        return rc;
+    if (!out || !query || !key_cache || !value_cache || !block_tables || !context_lens)
+        return fail(MVME_EINVAL, "paged attention received a null pointer");
+    const size_t need = mvme_paged_attention_workspace_size(batch, q_heads, kv_heads, head_dim, block_size,
+                                                            table_width, partition_tokens);
+    if (need > kScratchBytes)
+        return fail(MVME_EWORKSPACE, "paged attention (no-alloc) needs " + std::to_string(need) +
+                                         " bytes of split-K scratch, above its fixed " +
+                                         std::to_string(kScratchBytes) + "; use mvme_paged_attention");
+    void* workspace = nullptr;
+    if (need > 0)
+        if (int rc = device_scratch(&workspace)) return rc;
+    return launch_paged_attention(out, query, key_cache, value_cache, block_tables, context_lens, batch,
+                                  q_heads, kv_heads, head_dim, num_blocks, block_size, table_width,
+                                  partition_tokens, dtype, need, workspace, stream);
 }

@@ -35,6 +35,8 @@ SIGNATURES = {
     "mvme_paged_attention_workspace_size": (_size, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "mvme_paged_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
                                     _i64, _i64, _int, _vp, _size, _vp]),
+    "mvme_paged_attention_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                            _i64, _i64, _i64, _int, _vp]),
     "mvme_paged_prefill_workspace_size": (_size, [_i64] * 8),
     "mvme_paged_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _size, _vp]),

@@ -30,7 +30,7 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     symbols = declared_symbols()
-    assert len(symbols) == 14
+    assert len(symbols) == 15
     raw = ctypes.CDLL(str(hip_build.library_path()))
     for name in symbols:
         assert hasattr(raw, name), name
@@ -82,6 +82,20 @@ def test_decode_rejects_bad_arguments_before_launch(lib):
     assert status == ext.EWORKSPACE and "workspace" in lib.last_error()
     assert _status(lib, "mvme_paged_attention", None, 1, 1, 1, 1, 1, 2, 16, 8, 128, 4, 16, 2, 0, 0, None, 0,
                    None) == ext.EINVAL
+
+
+def test_noalloc_decode_rejects_before_touching_the_device(lib):
+    """The allocation-free decode entry checks shapes and its fixed 8 MiB
+    scratch limit before any HIP call (this container has no GPU)."""
+    def call(batch, width, partition, **kw):
+        return _status(lib, "mvme_paged_attention_noalloc", kw.get("out", 1), 1, 1, 1, 1, 1, batch, 16, 8, 128,
+                       4096, 256, width, partition, kw.get("dtype", 0), None)
+
+    assert lib.workspace_size(64, 16, 8, 128, 256, 64, 64) > 8 << 20
+    assert call(64, 64, 64) == ext.EWORKSPACE
+    assert "8388608" in lib.last_error() and "no-alloc" in lib.last_error()
+    assert call(2, 16, 0, dtype=7) == ext.EINVAL and "FP16/BF16" in lib.last_error()
+    assert call(2, 16, 0, out=None) == ext.EINVAL and "null pointer" in lib.last_error()
 
 
 def test_scatter_and_prefill_reject_bad_arguments(lib):
