@@ -336,7 +336,7 @@ class CpuLeg:
 # Other workloads of the path (reported under "extra").
 # ---------------------------------------------------------------------------
 
-EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "norm_rope", "after_attention")
+EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "kv_scatter", "norm_rope", "after_attention")
 
 
 def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, cpu,
@@ -351,6 +351,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra)
     if "prefill" in names:
         _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra)
+    if "kv_scatter" in names:
+        _extra_kv_scatter(torch, write_kv_cache_slots, workloads, cpu, dev, extra)
     if "norm_rope" in names:
         _extra_norm_rope(torch, cpu, dev, extra)
     if "after_attention" in names:
@@ -458,6 +460,35 @@ def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloa
         "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "GBps": kv_bytes / per_call / 1e9, "flops": flops, "priors": c["priors"],
         "max_abs_error": err}
+
+
+def _extra_kv_scatter(torch, write_kv_cache_slots, workloads, cpu, dev, extra):
+    """The KV scatter alone (write_kv_cache_slots): the chunked-prefill workload's
+    1,024 new rows (bf16, block 256) and the B8 decode workload's 8 rows (bf16,
+    block 16, 2048-page pool).  Algorithmic bytes per row: K and V read and
+    written (4 x 2,048 B at Hkv 8 / D 128) plus the 8-byte slot."""
+    cases = (("kv_scatter_prefill_1024_rows_bf16", workloads.chunked_prefill_case(device=dev), 100),
+             ("kv_scatter_decode_b8_8_rows_bf16", workloads.decode_b8_with_scatter(dev), 100))
+    for name, c, n in cases:
+        kc, vc, slots, nk, nv = c["key_cache"], c["value_cache"], c["slot_mapping"], c["new_key"], c["new_value"]
+        fn = lambda: write_kv_cache_slots(kc, vc, slots, nk, nv, backend="hip", validate=False)  # noqa: E731
+
+        def many(run_fn=fn, count=n):
+            def run():
+                for _ in range(count):
+                    run_fn()
+            return run
+        ms, _ = graph_time_ms(many(), torch, calls_per_graph=n, replays=20, warmup=3)
+        rows = slots.numel()
+        moved = rows * (4 * HKV * D * 2 + 8)
+        per_call = ms / n * 1e-3
+        flat_k = kc.view(-1, HKV, D)[slots].cpu()
+        flat_v = vc.view(-1, HKV, D)[slots].cpu()
+        extra[name] = {"us_per_call": per_call * 1e6, "GBps": moved / per_call / 1e9,
+                       "frac_of_hbm_peak": moved / per_call / 1e9 / HBM_PEAK_GBS, "rows": rows,
+                       "algorithmic_bytes": moved,
+                       "rows_bit_exact": bool(torch.equal(flat_k, nk.cpu()) and torch.equal(flat_v, nv.cpu()))}
+        del c
 
 
 def _norm_rope_case(torch, dev, tokens, dtype, seed):
@@ -608,6 +639,31 @@ def _extra_after_attention(torch, cpu, dev, extra):
                        bool(torch.equal(tokens.cpu(), cpu.greedy(logits.cpu())))}
 
 
+def summarize_headline_trace(path, steps, warmup):
+    """Average duration of the headline decode kernel over the timed graph replays.
+
+    In a headline-only run, headline() dispatches the 28 layer calls once
+    eagerly (before capture), then `warmup` untimed replays, then the `steps`
+    timed replays, then 4 eager repetitions for the wall-clock figure; the
+    timed dispatches are therefore positions [28 (1 + warmup), 28 (1 + warmup
+    + steps)) of the decode kernel's dispatches in start-time order."""
+    import csv
+
+    with open(path, newline="") as f:
+        rows = [r for r in csv.DictReader(f) if "paged_decode_kernel" in r["Kernel_Name"]]
+    rows.sort(key=lambda r: int(r["Start_Timestamp"]))
+    first, last = LAYERS * (1 + warmup), LAYERS * (1 + warmup + steps)
+    if len(rows) < last:
+        raise SystemExit(f"{path}: {len(rows)} decode dispatches, expected at least {last}")
+    timed = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows[first:last]]
+    every = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3 for r in rows]
+    span = (int(rows[last - 1]["End_Timestamp"]) - int(rows[first]["Start_Timestamp"])) / 1e3
+    return {"kernel": rows[first]["Kernel_Name"][:96], "dispatches": len(rows), "timed_dispatches": len(timed),
+            "timed_avg_us": statistics.mean(timed), "timed_min_us": min(timed), "timed_max_us": max(timed),
+            "timed_avg_x28_ms": statistics.mean(timed) * LAYERS / 1e3,
+            "timed_span_per_step_ms": span / steps / 1e3, "all_avg_us": statistics.mean(every)}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -622,7 +678,13 @@ def main(argv=None):
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU-baseline timing")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 10 plain 1 GiB device copies (scale reference for HBM byte counters)")
+    ap.add_argument("--trace-summary", metavar="KERNEL_TRACE_CSV",
+                    help="summarise a rocprofv3 kernel trace of a headline-only run (--no-extra) made with the "
+                         "same --steps/--warmup: the headline kernel's average over the timed replays only")
     args = ap.parse_args(argv)
+    if args.trace_summary:
+        print(json.dumps(summarize_headline_trace(args.trace_summary, args.steps, args.warmup)))
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU: the paged-attention path runs on a single MI355X and "
               f"--gpus {args.gpus} is not supported (decode would shard by sequence or kv head with no "
