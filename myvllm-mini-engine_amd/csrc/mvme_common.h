@@ -106,6 +106,29 @@ __device__ inline float group_sum(float v) {
     return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave, all in DPP (no LDS
+// round trip): shifts by 1, 2, 4, 8 inside each 16-lane row, then the row
+// totals carried forward by the row broadcasts of lane 15 (to rows 1 and 3)
+// and lane 31 (to rows 2 and 3).  Lanes a shift or a row mask leaves
+// unwritten take 0.
+__device__ inline int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);  // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);  // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);  // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);  // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);  // row_bcast:31
+    return x;
+}
+
+// Value of lane `l` (wave-uniform index) for every lane.
+__device__ inline int lane_value(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ inline int64_t lane_value(int64_t v, int l) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), l);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 constexpr float kLog2e = 1.4426950408889634f;

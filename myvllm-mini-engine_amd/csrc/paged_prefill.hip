@@ -194,22 +194,17 @@ __device__ inline bool find_item(const PrefillArgs& a, int chunk_len, int item, 
         const SeqMeta m = (first && s0 == 0) ? *first : load_meta(a, s0 + lane);
         const int64_t row0 = m.row0, n = m.n, start = m.start, ctx = m.ctx;
         const int cnt = seq_items(a, chunk_len, n, start, ctx);
-        int incl = cnt;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const int other = __shfl_up(incl, off);
-            if (lane >= off) incl += other;
-        }
-        const int total = __shfl(incl, kWave - 1);
+        const int incl = wave_incl_scan(cnt);
+        const int total = lane_value(incl, kWave - 1);
         if (!found && item >= base && item < base + total) {
             const uint64_t hit = __ballot(base + incl > item);
             const int sel = __builtin_ctzll(hit);
             it.seq = s0 + sel;
-            int rem = item - base - (__shfl(incl, sel) - __shfl(cnt, sel));
-            it.row0 = __shfl(row0, sel);
-            it.qlen = __shfl(n, sel);
-            it.start = __shfl(start, sel);
-            it.ctx = __shfl(ctx, sel);
+            int rem = item - base - (lane_value(incl, sel) - lane_value(cnt, sel));
+            it.row0 = lane_value(row0, sel);
+            it.qlen = lane_value(n, sel);
+            it.start = lane_value(start, sel);
+            it.ctx = lane_value(ctx, sel);
             // Query blocks from the last (longest key range) to the first, so
             // that the work-groups dispatched last are the short ones.
             const int64_t nblocks = (it.qlen + a.qb - 1) / a.qb;
@@ -353,18 +348,13 @@ struct PrefillLds {
 __device__ inline int walk_index(const PrefillArgs& a, int chunk_len, const SeqMeta& m, PrefillLds& lds) {
     const int lane = __lane_id();
     const int cnt = seq_items(a, chunk_len, m.n, m.start, m.ctx);
-    int incl = cnt;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const int other = __shfl_up(incl, off);
-        if (lane >= off) incl += other;
-    }
+    const int incl = wave_incl_scan(cnt);
     if (threadIdx.x < kWave) {
         lds.meta[lane] = m;
         lds.cnt[lane] = cnt;
         lds.incl[lane] = incl;
     }
-    return __shfl(incl, kWave - 1);
+    return lane_value(incl, kWave - 1);
 }
 
 __device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, int total, const PrefillLds& lds,
@@ -374,12 +364,12 @@ __device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, in
     const SeqMeta m = lds.meta[lane];
     const int cnt = lds.cnt[lane], incl_s = lds.incl[lane];
     const int sel = __builtin_ctzll(__ballot(incl_s > item));
-    int rem = item - (__shfl(incl_s, sel) - __shfl(cnt, sel));
+    int rem = item - (lane_value(incl_s, sel) - lane_value(cnt, sel));
     it.seq = sel;
-    it.row0 = __shfl(m.row0, sel);
-    it.qlen = __shfl(m.n, sel);
-    it.start = __shfl(m.start, sel);
-    it.ctx = __shfl(m.ctx, sel);
+    it.row0 = lane_value(m.row0, sel);
+    it.qlen = lane_value(m.n, sel);
+    it.start = lane_value(m.start, sel);
+    it.ctx = lane_value(m.ctx, sel);
     it.chunk_len = chunk_len;
     // Query blocks from the last to the first (as find_item), 64 at a time:
     // lane l takes the l-th block of the group.
@@ -392,19 +382,14 @@ __device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, in
             e = block_kv_end(a, it.start, it.ctx, it.qlen, bi * a.qb);
             nc = chunks_of(chunk_len, e);
         }
-        int incl = nc;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-            const int other = __shfl_up(incl, off);
-            if (lane >= off) incl += other;
-        }
-        const int group = __shfl(incl, kWave - 1);
+        const int incl = wave_incl_scan(nc);
+        const int group = lane_value(incl, kWave - 1);
         if (rem < group) {
             const int l = __builtin_ctzll(__ballot(incl > rem));
             it.q0 = (int)((nblocks - 1 - (g0 + l)) * a.qb);
-            it.chunk = rem - (__shfl(incl, l) - __shfl(nc, l));
-            it.kv_end = __shfl(e, l);
-            it.nchunks = __shfl(nc, l);
+            it.chunk = rem - (lane_value(incl, l) - lane_value(nc, l));
+            it.kv_end = lane_value(e, l);
+            it.nchunks = lane_value(nc, l);
             return true;
         }
         rem -= group;
@@ -471,13 +456,19 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             pos[nb] = -1;
         }
     }
+    // Wave maximum / minimum: the lanes of one MFMA row index li hold the
+    // same rows, so lanes 0..15 cover every row of the wave (readlane, no
+    // LDS round trips).
+    {
+        int hi = wave_last, lo = wave_first;
 #pragma unroll
-    for (int mask = 1; mask < kWave; mask <<= 1) {
-        wave_last = max(wave_last, __shfl_xor(wave_last, mask));
-        wave_first = min(wave_first, __shfl_xor(wave_first, mask));
+        for (int l = 0; l < 16; ++l) {
+            hi = max(hi, lane_value(wave_last, l));
+            lo = min(lo, lane_value(wave_first, l));
+        }
+        wave_last = __builtin_amdgcn_readfirstlane(hi);
+        wave_first = __builtin_amdgcn_readfirstlane(lo);
     }
-    wave_last = __builtin_amdgcn_readfirstlane(wave_last);
-    wave_first = __builtin_amdgcn_readfirstlane(wave_first);
 
 
     // m_run: the row's reference (log2 units, -inf until the row sees a key);
@@ -537,13 +528,34 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         const int64_t page = ctable[idx];
         return (key < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
     };
+    // Page-per-tile mode: the page ids of 64 consecutive tiles, one per lane
+    // (lane j: tile tile_base + j; -1 when absent or past the chunk), loaded
+    // with one vector load per 64 tiles and read with readlane -- the tile
+    // loop never waits for a table lookup.
+    int tile_base = t_begin, tile_pages = -1;
+    auto load_tile_pages = [&](int base) {
+        const int key0 = (base + lane) * kPfKeys;
+        int pg = -1;
+        if (key0 < chunk_end) {
+            const int64_t page = table[key0 >> bs_shift];
+            pg = (page >= 0 && page < a.num_blocks) ? (int)page : -1;
+        }
+        tile_pages = pg;
+        tile_base = base;
+    };
+    // Tiles are looked up in increasing order, so the window only moves forward.
+    auto page_of_tile = [&](int tile) -> int {
+        if (tile >= tile_base + kWave) load_tile_pages(tile);
+        return __builtin_amdgcn_readlane(tile_pages, tile - tile_base);
+    };
+    if constexpr (PAGES == kPagesPerTile) load_tile_pages(t_begin);
+    // Bit st: the tile in ring stage st lies in one present page with all of
+    // its 64 keys in the chunk (set by every wave when it issues the copies).
+    uint32_t full_stages = 0;
     int pg_next[kPfIpw];  // pages for the next tile to issue
     auto lookup = [&](int tile) {
         if constexpr (PAGES == kPagesPerTile) {
-            // The whole tile lies in one page (-1 when absent or past the chunk).
-            const int key0 = tile * kPfKeys;
-            const int64_t page = ctable[(key0 < cap ? key0 : cap - 1) >> bs_shift];
-            const int pg = (key0 < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
+            const int pg = page_of_tile(tile);
 #pragma unroll
             for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pg;
         } else {
@@ -557,7 +569,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     auto issue = [&](int tile, int st) {
         if constexpr (PAGES == kPagesPerTile) {
             const int key0 = tile * kPfKeys;
-            if (pg_next[0] >= 0 && key0 + kPfKeys - 1 < chunk_end) {
+            const bool full = pg_next[0] >= 0 && key0 + kPfKeys - 1 < chunk_end;
+            full_stages = full ? (full_stages | (1u << st)) : (full_stages & ~(1u << st));
+            if (full) {
                 // Full tile in one page: one scalar base for all copies.
                 const int64_t base =
                     (int64_t)pg_next[0] * page_bytes_g + (int64_t)(key0 & (a.block_size - 1)) * row_bytes_g;
@@ -568,7 +582,6 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     lds_dma16_s(kcache + base, tile_off[i], lk + 1024 * j);
                     lds_dma16_s(vcache + base, tile_off_v[i], lv + 1024 * j);
                 }
-                if (lane == 0) sm_full[st][wave] = 1;
                 return;
             }
         }
@@ -600,16 +613,6 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         if (lane == 0) sm_full[st][wave] = wave_full ? 1 : 0;
     };
 
-    // Page ids of the first tiles (scalar loads) go out before the Q loads
-    // so that both latencies overlap.
-    int pro_pg[2];
-    if constexpr (PAGES == kPagesPerTile) {
-#pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            lookup(t_begin + k);
-            pro_pg[k] = pg_next[0];
-        }
-    }
     // Q^T operands: row (nb, li), d = 32*dc + 8*lg .. +8.  Their latency
     // overlaps the first pair's copies: the first pair barrier waits for the
     // whole vector-memory counter.
@@ -628,13 +631,10 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     if (t_begin < t_end) {
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            if constexpr (PAGES == kPagesPerTile) {
-#pragma unroll
-                for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pro_pg[k];
-            } else {
+            if (t_begin + k < t_end) {
                 lookup(t_begin + k);
+                issue(t_begin + k, k);
             }
-            issue(t_begin + k, k);
         }
     }
     for (int tp = t_begin; tp < t_end; tp += 2) {
@@ -645,8 +645,10 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         landed_barrier();
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            lookup(tp + 2 + k);
-            issue(tp + 2 + k, (st0 + 2 + k) & (kPfStages - 1));
+            if (tp + 2 + k < t_end) {  // stages of tiles past the chunk are never read
+                lookup(tp + 2 + k);
+                issue(tp + 2 + k, (st0 + 2 + k) & (kPfStages - 1));
+            }
         }
         // Unrolled: with this loop left rolled, the compiler's wait insertion
         // puts a full vmcnt(0) at its head (before the first product of every
@@ -662,10 +664,15 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 const float* smb = &sm_b[st][0];
                 // Every key of the tile present and visible to every row of the
                 // wave: no bias and no causal mask needed.
-                static_assert(kPfWaves == 8, "two int4 flag reads below");
-                const int4 fa = *reinterpret_cast<const int4*>(&sm_full[st][0]);
-                const int4 fb = *reinterpret_cast<const int4*>(&sm_full[st][4]);
-                const bool full = (fa.x & fa.y & fa.z & fa.w & fb.x & fb.y & fb.z & fb.w) != 0;
+                bool full;
+                if constexpr (PAGES == kPagesPerTile) {
+                    full = ((full_stages >> st) & 1u) != 0;
+                } else {
+                    static_assert(kPfWaves == 8, "two int4 flag reads below");
+                    const int4 fa = *reinterpret_cast<const int4*>(&sm_full[st][0]);
+                    const int4 fb = *reinterpret_cast<const int4*>(&sm_full[st][4]);
+                    full = (fa.x & fa.y & fa.z & fa.w & fb.x & fb.y & fb.z & fb.w) != 0;
+                }
                 const bool fast = full && tile0 + kPfKeys - 1 <= wave_first;
                 typedef __attribute__((address_space(3))) uint8_t lds_u8;
                 lds_u8* vbase = (lds_u8*)&sm_v[st][0];
