@@ -528,27 +528,28 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         const int64_t page = ctable[idx];
         return (key < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
     };
-    // Page-per-tile mode: the page ids of 64 consecutive tiles, one per lane
-    // (lane j: tile tile_base + j; -1 when absent or past the chunk), loaded
-    // with one vector load per 64 tiles and read with readlane -- the tile
-    // loop never waits for a table lookup.
-    int tile_base = t_begin, tile_pages = -1;
-    auto load_tile_pages = [&](int base) {
+    // Page-per-tile mode: the page ids of a window of 64 consecutive tiles,
+    // one per lane (lane j: tile tile_base + j; -1 when absent or past the
+    // chunk), read with readlane -- the tile loop never waits for a table
+    // lookup.  The next window is loaded one window ahead (right after the
+    // copies that follow a switch), so by its first use a barrier's full wait
+    // has retired it.  Windows start at t_begin + 64 k: both tiles of a pair
+    // lie in one window.
+    // Raw table entries are kept (validated at use), so that nothing waits for
+    // the window's load before the tile loop needs it.
+    int tile_base = t_begin;
+    int64_t tile_pages = -1, next_pages = -1;
+    auto window_pages = [&](int base) -> int64_t {
         const int key0 = (base + lane) * kPfKeys;
-        int pg = -1;
-        if (key0 < chunk_end) {
-            const int64_t page = table[key0 >> bs_shift];
-            pg = (page >= 0 && page < a.num_blocks) ? (int)page : -1;
-        }
-        tile_pages = pg;
-        tile_base = base;
+        int64_t raw = -1;
+        if (key0 < chunk_end) raw = table[key0 >> bs_shift];
+        return raw;
     };
-    // Tiles are looked up in increasing order, so the window only moves forward.
     auto page_of_tile = [&](int tile) -> int {
-        if (tile >= tile_base + kWave) load_tile_pages(tile);
-        return __builtin_amdgcn_readlane(tile_pages, tile - tile_base);
+        const int64_t page = lane_value(tile_pages, tile - tile_base);
+        return (page >= 0 && page < a.num_blocks) ? (int)page : -1;
     };
-    if constexpr (PAGES == kPagesPerTile) load_tile_pages(t_begin);
+    if constexpr (PAGES == kPagesPerTile) tile_pages = window_pages(t_begin);
     // Bit st: the tile in ring stage st lies in one present page with all of
     // its 64 keys in the chunk (set by every wave when it issues the copies).
     uint32_t full_stages = 0;
@@ -637,12 +638,22 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             }
         }
     }
+    if constexpr (PAGES == kPagesPerTile)
+        if (t_begin + kWave < t_end) next_pages = window_pages(t_begin + kWave);
     for (int tp = t_begin; tp < t_end; tp += 2) {
         const int st0 = (tp - t_begin) & (kPfStages - 1);
         // Both tiles of the pair have landed (this lane's copies, then every
         // lane's through the barrier), and every wave is done with the
         // previous pair, whose stages the copies below refill.
         landed_barrier();
+        bool switched = false;
+        if constexpr (PAGES == kPagesPerTile) {
+            if (tp + 2 >= tile_base + kWave && tp + 2 < t_end) {
+                tile_pages = next_pages;
+                tile_base += kWave;
+                switched = true;
+            }
+        }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
             if (tp + 2 + k < t_end) {  // stages of tiles past the chunk are never read
@@ -650,6 +661,8 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 issue(tp + 2 + k, (st0 + 2 + k) & (kPfStages - 1));
             }
         }
+        if constexpr (PAGES == kPagesPerTile)
+            if (switched && tile_base + kWave < t_end) next_pages = window_pages(tile_base + kWave);
         // Unrolled: with this loop left rolled, the compiler's wait insertion
         // puts a full vmcnt(0) at its head (before the first product of every
         // tile), and that wait also covers the copies issued just above, so
