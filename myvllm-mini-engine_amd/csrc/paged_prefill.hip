@@ -628,37 +628,48 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         }
     }
 
-    // Prologue: the first pair of tiles in flight.
+    // Prologue: only the first tile in flight, so the first products wait
+    // for the queries and one tile; the pairs that follow are (t, t+1) with
+    // t - t_begin odd, each issued one pair ahead.
     if (t_begin < t_end) {
+        if constexpr (PAGES == kPagesPerTile) {
+            // A scalar lookup: the window's vector load is first needed after
+            // the first barrier, so nothing waits for it (or for the queries)
+            // before these copies go out.
+            const int key0 = t_begin * kPfKeys;
+            const int64_t page = ctable[key0 >> bs_shift];
+            const int pg = (key0 < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
-            if (t_begin + k < t_end) {
-                lookup(t_begin + k);
-                issue(t_begin + k, k);
-            }
+            for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pg;
+        } else {
+            lookup(t_begin);
         }
+        issue(t_begin, 0);
     }
     if constexpr (PAGES == kPagesPerTile)
         if (t_begin + kWave < t_end) next_pages = window_pages(t_begin + kWave);
-    for (int tp = t_begin; tp < t_end; tp += 2) {
+    for (int tp = t_begin - 1; tp < t_end; tp += 2) {
         const int st0 = (tp - t_begin) & (kPfStages - 1);
         // Both tiles of the pair have landed (this lane's copies, then every
         // lane's through the barrier), and every wave is done with the
         // previous pair, whose stages the copies below refill.
         landed_barrier();
         bool switched = false;
-        if constexpr (PAGES == kPagesPerTile) {
-            if (tp + 2 >= tile_base + kWave && tp + 2 < t_end) {
-                tile_pages = next_pages;
-                tile_base += kWave;
-                switched = true;
-            }
-        }
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
-            if (tp + 2 + k < t_end) {  // stages of tiles past the chunk are never read
-                lookup(tp + 2 + k);
-                issue(tp + 2 + k, (st0 + 2 + k) & (kPfStages - 1));
+            const int tile = tp + 2 + k;
+            if (tile < t_end) {  // stages of tiles past the chunk are never read
+                if constexpr (PAGES == kPagesPerTile) {
+                    // The next window was loaded a window ago; the barrier's
+                    // full wait has retired it.
+                    if (tile >= tile_base + kWave) {
+                        tile_pages = next_pages;
+                        tile_base += kWave;
+                        switched = true;
+                    }
+                }
+                lookup(tile);
+                issue(tile, (st0 + 2 + k) & (kPfStages - 1));
             }
         }
         if constexpr (PAGES == kPagesPerTile)
@@ -670,6 +681,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 #pragma unroll
         for (int k = 0; k < 2 && tp + k < t_end; ++k) {
             const int tile = tp + k;
+            if (tile < t_begin) continue;  // the prologue's virtual first slot
             const int st = (st0 + k) & (kPfStages - 1);
             const int tile0 = tile * kPfKeys;
             if (tile0 <= wave_last) {

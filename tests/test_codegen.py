@@ -46,14 +46,19 @@ def kernels(asm):
 
 def stray_waits(ins):
     """Full vmcnt waits between a barrier and the first MFMA after it, other
-    than the wait that directly precedes a barrier."""
-    stray, armed, pending = [], False, None
+    than the wait that directly precedes a barrier, issued while tile copies
+    (global_load_lds) are in flight -- a full wait with no copy outstanding
+    (e.g. for an item's metadata before its first copy) delays nothing."""
+    stray, armed, pending, copies = [], False, None, False
     for i, s in enumerate(ins):
+        if s.startswith("global_load_lds"):
+            copies = True
         if s.startswith("s_barrier"):
             armed, pending = True, None
-        elif armed and s.startswith("s_waitcnt") and "vmcnt(0)" in s:
-            if not (i + 1 < len(ins) and ins[i + 1].startswith("s_barrier")):
+        elif s.startswith("s_waitcnt") and "vmcnt(0)" in s:
+            if armed and copies and not (i + 1 < len(ins) and ins[i + 1].startswith("s_barrier")):
                 pending = (i, s)
+            copies = False
         elif armed and s.startswith("v_mfma"):
             if pending:
                 stray.append(pending)
@@ -77,3 +82,6 @@ def test_stray_wait_detector_flags_a_planted_wait():
     assert stray_waits(clean) == []
     planted = clean[:3] + ["s_waitcnt vmcnt(0) lgkmcnt(3)"] + clean[4:]
     assert stray_waits(planted) == [(3, "s_waitcnt vmcnt(0) lgkmcnt(3)")]
+    # A full wait before any copy of the barrier's interval is issued is harmless.
+    early = clean[:2] + ["s_waitcnt vmcnt(0)"] + clean[2:]
+    assert stray_waits(early) == []
