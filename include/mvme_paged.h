@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MVME_ABI_VERSION 1
+#define MVME_ABI_VERSION 2
 
 /* Element types of the KV cache, queries and outputs (FP32: sampling logits only). */
 enum mvme_dtype { MVME_FP16 = 0, MVME_BF16 = 1, MVME_FP32 = 2 };
@@ -169,12 +169,15 @@ int mvme_paged_attention_noalloc(void* out, const void* query,
 
 /*
  * Bytes of device workspace mvme_paged_prefill_attention needs for these
- * shapes (0 when no query block is split over key chunks).  Pure host
- * function.  chunk_tokens: 0 selects the library's default key chunking.
+ * shapes and element type (0 when no query block is split over key chunks).
+ * Pure host function.  chunk_tokens: 0 selects the library's default key
+ * chunking.  Layout: the key-chunk partial outputs (2-byte elements for
+ * MVME_BF16, 4-byte for MVME_FP16), their fp32 (reference, sum) pairs, and
+ * one int per packed token.
  */
 size_t mvme_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
                                          int64_t kv_heads, int64_t head_dim, int64_t block_size,
-                                         int64_t table_width, int64_t chunk_tokens);
+                                         int64_t table_width, int64_t chunk_tokens, int dtype);
 
 /*
  * Ragged chunked paged prefill: packed queries q[total_tokens, q_heads,

@@ -1221,6 +1221,9 @@ __global__ __launch_bounds__(kWave) void paged_prefill_generic_kernel(PrefillArg
     }
 }
 
+constexpr int64_t kMaxPrefillRows = 2147483647;  // packed rows x heads, table capacity
+constexpr int64_t kMaxPrefillSeqs = 65535 * 16;
+
 int check_prefill(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64_t kv_heads,
                   int64_t head_dim, int64_t num_blocks, int64_t block_size, int64_t table_width,
                   int dtype) {
@@ -1231,8 +1234,9 @@ int check_prefill(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64
         return fail(MVME_EINVAL, "paged prefill GQA/head_dim mismatch (maximum head_dim 1024)");
     if (num_seqs < 0 || total_tokens < 0 || table_width < 0)
         return fail(MVME_EINVAL, "paged prefill metadata shape mismatch");
-    if (total_tokens * q_heads > 2147483647) return fail(MVME_EINVAL, "too many paged prefill rows");
-    if (num_seqs > 65535 * 16) return fail(MVME_EINVAL, "too many paged prefill sequences");
+    if (total_tokens > kMaxPrefillRows || q_heads > kMaxPrefillRows || total_tokens * q_heads > kMaxPrefillRows)
+        return fail(MVME_EINVAL, "too many paged prefill rows");
+    if (num_seqs > kMaxPrefillSeqs) return fail(MVME_EINVAL, "too many paged prefill sequences");
     return MVME_OK;
 }
 
@@ -1279,6 +1283,23 @@ PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_
     return p;
 }
 
+// Key-chunk workspace: the partial outputs [max_chunks][rows][D] in the
+// partial type (bf16 for bf16 inputs, fp32 for fp16), their (reference,
+// sum) pairs [max_chunks][rows][2] fp32, then one int per packed token; each
+// region 16-byte aligned.
+struct PrefillWorkspace {
+    size_t ml_offset, tok_offset, bytes;
+};
+PrefillWorkspace prefill_workspace_layout(int64_t rows, int64_t max_chunks, int64_t tokens, int dtype) {
+    const size_t part_elem = dtype == MVME_BF16 ? sizeof(uint16_t) : sizeof(float);
+    auto align16 = [](size_t n) { return (n + 15) / 16 * 16; };
+    PrefillWorkspace w{};
+    w.ml_offset = align16((size_t)max_chunks * rows * kPfD * part_elem);
+    w.tok_offset = w.ml_offset + align16((size_t)max_chunks * rows * 2 * sizeof(float));
+    w.bytes = w.tok_offset + align16((size_t)tokens * sizeof(int));
+    return w;
+}
+
 }  // namespace
 }  // namespace mvme
 
@@ -1286,16 +1307,19 @@ using namespace mvme;
 
 extern "C" size_t mvme_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
                                                     int64_t kv_heads, int64_t head_dim, int64_t block_size,
-                                                    int64_t table_width, int64_t chunk_tokens) {
+                                                    int64_t table_width, int64_t chunk_tokens, int dtype) {
     if (num_seqs <= 0 || total_tokens <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 ||
-        block_size <= 0 || table_width <= 0)
+        block_size <= 0 || table_width <= 0 || !valid_dtype(dtype))
+        return 0;
+    // The limits the entry point enforces; inside them no product overflows.
+    if (total_tokens > kMaxPrefillRows || q_heads > kMaxPrefillRows || total_tokens * q_heads > kMaxPrefillRows ||
+        block_size > kMaxPrefillRows || table_width > kMaxPrefillRows ||
+        table_width * block_size > kMaxPrefillRows || num_seqs > kMaxPrefillSeqs)
         return 0;
     const PrefillPlan p = make_prefill_plan(num_seqs, total_tokens, q_heads, kv_heads, head_dim, block_size,
                                             table_width, chunk_tokens);
     if (!p.mfma || p.max_chunks <= 1) return 0;
-    // Partials (O, then max/sum), then one int per token, 16-byte aligned.
-    const size_t partials = (size_t)total_tokens * q_heads * p.max_chunks * (kPfD + 2) * sizeof(float);
-    return partials + ((size_t)total_tokens * sizeof(int) + 15) / 16 * 16;
+    return prefill_workspace_layout(total_tokens * q_heads, p.max_chunks, total_tokens, dtype).bytes;
 }
 
 extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void* key_cache,
@@ -1315,7 +1339,7 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         !context_lens)
         return fail(MVME_EINVAL, "paged prefill received a null pointer");
     const size_t need = mvme_paged_prefill_workspace_size(num_seqs, total_tokens, q_heads, kv_heads, head_dim,
-                                                          block_size, table_width, chunk_tokens);
+                                                          block_size, table_width, chunk_tokens, dtype);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))
         return fail(MVME_EWORKSPACE, "paged prefill workspace too small: need " + std::to_string(need) +
                                          " bytes, got " + std::to_string(workspace_bytes));
@@ -1351,9 +1375,11 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         a.total_tokens = total_tokens;
         a.chunk_choice = chunk_tokens <= 0 ? 1 : 0;
         if (need > 0) {
+            const PrefillWorkspace w = prefill_workspace_layout(total_tokens * q_heads, p.max_chunks, total_tokens,
+                                                                dtype);
             a.ws_o = workspace;
-            a.ws_ml = static_cast<float*>(workspace) + total_tokens * q_heads * p.max_chunks * kPfD;
-            a.ws_tok = reinterpret_cast<int*>(a.ws_ml + total_tokens * q_heads * p.max_chunks * 2);
+            a.ws_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + w.ml_offset);
+            a.ws_tok = reinterpret_cast<int*>(static_cast<uint8_t*>(workspace) + w.tok_offset);
         }
         // The item count depends on lengths that stay on the device, so the
         // grid is sized from a bound.  With key splitting that bound is loose

@@ -16,7 +16,7 @@ from .. import build as _build
 
 FP16, BF16, FP32 = 0, 1, 2
 OK, EINVAL, ELAUNCH, EWORKSPACE = 0, 1, 2, 3
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _i64, _vp, _int, _size = ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
 
@@ -37,7 +37,7 @@ SIGNATURES = {
                                     _i64, _i64, _int, _vp, _size, _vp]),
     "mvme_paged_attention_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _int, _vp]),
-    "mvme_paged_prefill_workspace_size": (_size, [_i64] * 8),
+    "mvme_paged_prefill_workspace_size": (_size, [_i64] * 8 + [_int]),
     "mvme_paged_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _size, _vp]),
     "mvme_qk_norm_rope_write_kv": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp,

@@ -76,7 +76,7 @@ def paged_prefill_attention(q, key_cache, value_cache, cu_seqlens_q, query_start
     num_blocks, _, kv_heads, head_dim = key_cache.shape
     num_seqs, width = query_starts.numel(), block_tables.shape[1]
     need = lib.prefill_workspace_size(num_seqs, q.shape[0], q.shape[1], kv_heads, head_dim, block_size, width,
-                                      chunk_tokens)
+                                      chunk_tokens, ext.dtype_code(q.dtype))
     if need and workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else 0

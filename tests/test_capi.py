@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version(lib):
-    assert lib._lib.mvme_abi_version() == ext.ABI_VERSION == 1
+    assert lib._lib.mvme_abi_version() == ext.ABI_VERSION == 2
 
 
 def test_workspace_size_is_a_host_function(lib):
@@ -108,12 +108,17 @@ def test_scatter_and_prefill_reject_bad_arguments(lib):
                    None, 0, None) == ext.EINVAL
     assert "1024" in lib.last_error()
     # Few query blocks + long table: key-chunk split needs a workspace.
-    need = lib.prefill_workspace_size(8, 1024, 16, 8, 128, 256, 16, 0)
+    need = lib.prefill_workspace_size(8, 1024, 16, 8, 128, 256, 16, 0, ext.FP16)
     assert need == 1024 * 16 * 8 * (128 + 2) * 4 + 1024 * 4
+    # bf16 inputs keep bf16 partials: 2 bytes per partial element.
+    assert lib.prefill_workspace_size(8, 1024, 16, 8, 128, 256, 16, 0, ext.BF16) == \
+        1024 * 16 * 8 * (128 * 2 + 2 * 4) + 1024 * 4
+    assert lib.prefill_workspace_size(8, 1024, 16, 8, 128, 256, 16, 0, 9) == 0  # no such type
+    assert lib.prefill_workspace_size(8, 1 << 40, 1 << 30, 8, 128, 256, 16, 0, ext.BF16) == 0  # refused shape
     assert _status(lib, "mvme_paged_prefill_attention", 1, 1, 1, 1, 1, 1, 1, 1, 8, 1024, 16, 8, 128, 200, 256, 16,
                    0, 0, None, 0, None) == ext.EWORKSPACE
     # Many query blocks: no split, no workspace.
-    assert lib.prefill_workspace_size(8, 1 << 16, 16, 8, 128, 256, 16, 0) == 0
+    assert lib.prefill_workspace_size(8, 1 << 16, 16, 8, 128, 256, 16, 0, ext.BF16) == 0
     # Empty inputs are legal no-ops.
     assert _status(lib, "mvme_write_kv_cache_slots", 1, 1, 4, 16, 8, 128, None, None, None, 0, 1024, 1024, 1,
                    None) == ext.OK
