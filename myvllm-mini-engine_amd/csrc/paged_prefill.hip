@@ -345,10 +345,11 @@ struct PrefillLds {
 // prefixes plus a lane-parallel search over the sequence's query blocks.
 // walk_index returns the item total; wave 0 stores the index in LDS (read
 // after the next barrier).
-__device__ inline int walk_index(const PrefillArgs& a, int chunk_len, const SeqMeta& m, PrefillLds& lds) {
+__device__ inline int walk_index(const PrefillArgs& a, int chunk_len, const SeqMeta& m, PrefillLds& lds,
+                                int& cnt, int& incl) {
     const int lane = __lane_id();
-    const int cnt = seq_items(a, chunk_len, m.n, m.start, m.ctx);
-    const int incl = wave_incl_scan(cnt);
+    cnt = seq_items(a, chunk_len, m.n, m.start, m.ctx);
+    incl = wave_incl_scan(cnt);
     if (threadIdx.x < kWave) {
         lds.meta[lane] = m;
         lds.cnt[lane] = cnt;
@@ -357,12 +358,12 @@ __device__ inline int walk_index(const PrefillArgs& a, int chunk_len, const SeqM
     return lane_value(incl, kWave - 1);
 }
 
-__device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, int total, const PrefillLds& lds,
-                                         int item, PrefillItem& it) {
+// Lookup from the index values every wave holds in its lanes (lane s:
+// sequence s's metadata, item count and inclusive prefix).
+__device__ inline bool find_item_lanes(const PrefillArgs& a, int chunk_len, int total, const SeqMeta& m, int cnt,
+                                       int incl_s, int item, PrefillItem& it) {
     if (item >= total) return false;
     const int lane = __lane_id();
-    const SeqMeta m = lds.meta[lane];
-    const int cnt = lds.cnt[lane], incl_s = lds.incl[lane];
     const int sel = __builtin_ctzll(__ballot(incl_s > item));
     int rem = item - (lane_value(incl_s, sel) - lane_value(cnt, sel));
     it.seq = sel;
@@ -395,6 +396,12 @@ __device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, in
         rem -= group;
     }
     return false;  // (only if the counts are inconsistent)
+}
+
+__device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, int total, const PrefillLds& lds,
+                                         int item, PrefillItem& it) {
+    const int lane = __lane_id();
+    return find_item_lanes(a, chunk_len, total, lds.meta[lane], lds.cnt[lane], lds.incl[lane], item, it);
 }
 
 
@@ -858,7 +865,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         if (qi[nb] >= qlen) continue;
         const int64_t rowid = (row0 + qi[nb]) * a.q_heads + head[nb];
         if (nchunks == 1) {
-            const float inv = (row_ok[nb] && l_row > 0.f) ? 1.f / l_row : 0.f;
+            const float inv = (row_ok[nb] && l_row > 0.f) ? __builtin_amdgcn_rcpf(l_row) : 0.f;
             uint16_t* orow = static_cast<uint16_t*>(a.out) + rowid * kPfD;
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
@@ -868,7 +875,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             }
         } else {
             const int64_t slot = (int64_t)chunk * a.ws_rows + rowid;
-            const float inv = (row_ok[nb] && l_row > 0.f) ? 1.f / l_row : 0.f;
+            const float inv = (row_ok[nb] && l_row > 0.f) ? __builtin_amdgcn_rcpf(l_row) : 0.f;
             using P = typename PartialOf<T>::type;
             P* po = static_cast<P*>(a.ws_o) + slot * kPfD;
 #pragma unroll
@@ -1004,14 +1011,16 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
         bool ok = false;
         if (indexed) {
             const SeqMeta m = load_meta(a, (int)(threadIdx.x & (kWave - 1)));
-            total = walk_index(a, chunk_len, m, lds);
+            int cnt, incl;
+            total = walk_index(a, chunk_len, m, lds, cnt, incl);
             if (a.chunk_choice && total > a.item_stride) {
                 // More than one round of items: the lengths decide the chunk.
                 chunk_len = choose_chunk(a, lds, m);
-                total = walk_index(a, chunk_len, m, lds);
+                total = walk_index(a, chunk_len, m, lds, cnt, incl);
             }
-            __syncthreads();  // the index is in LDS
-            ok = find_item_indexed(a, chunk_len, total, lds, idx, item);
+            // The first lookup uses this wave's own copy of the index; wave 0's
+            // LDS copy serves the later ones (after the barrier between items).
+            ok = find_item_lanes(a, chunk_len, total, m, cnt, incl, idx, item);
         } else {
             ok = find_item(a, chunk_len, idx, item, &total);
             if (a.chunk_choice && total > a.item_stride) {
