@@ -4,7 +4,10 @@ Restates the ownership semantics of the reference's ``BlockManager``
 (mini_engine/cache/block_manager.py:10-166) that decide which physical page
 ids appear in the block tables the kernels read: private pages are
 refcount 1, a cached prefix attached to several requests appears in each of
-their tables (refcount = number of holders).  Host-side only.
+their tables (refcount = number of holders), and a request can be given
+retained pages only (``attach``, block_manager.py:83-97 — the prefix cache's
+whole-prompt hit, prefix_cache.py:45-48), so its table holds no private
+page at all.  Host-side only.
 """
 
 from __future__ import annotations
@@ -44,9 +47,9 @@ class PagePool:
             self._refs[page] = 1
         return pages
 
-    def _check_live(self, pages) -> None:
+    def _check_live(self, pages, what="prefix") -> None:
         if len(set(pages)) != len(pages):
-            raise ValueError("pages must be distinct")
+            raise ValueError(f"{what} pages must be distinct")
         for page in pages:
             if page < 0 or page >= self.num_blocks or self._refs[page] <= 0:
                 raise ValueError(f"cannot attach unallocated block: {page}")
@@ -69,10 +72,21 @@ class PagePool:
         self._owned[request_id] = prefix + suffix
         return list(self._owned[request_id])
 
+    def attach(self, request_id: str, pages) -> list[int]:
+        """Give a request a table made only of pages other holders retain."""
+        if request_id in self._owned:
+            raise ValueError(f"request already owns blocks: {request_id}")
+        pages = [int(p) for p in pages]
+        self._check_live(pages, "attached")
+        for page in pages:
+            self._refs[page] += 1
+        self._owned[request_id] = pages
+        return list(pages)
+
     def pin(self, pages) -> None:
         """Hold one external reference (e.g. a prefix-cache entry)."""
         pages = list(pages)
-        self._check_live(pages)
+        self._check_live(pages, "pinned")
         for page in pages:
             self._refs[page] += 1
 

@@ -197,6 +197,33 @@ def test_page_pool_shared_prefix_refcounts():
         pool.allocate_with_prefix("e", 12, [a[2]])
 
 
+def test_page_pool_attach_retained_pages():
+    """block_manager.py:83-97: a request whose whole table is retained pages
+    (a prefix-cache hit covering the prompt) takes no free page, and its
+    release leaves the pages with their other holders."""
+    pool = PagePool(8, 4)
+    prefix = pool.allocate("prefix", 8)
+    pool.pin(prefix)
+    free = pool.free_blocks
+    assert pool.attach("hit", prefix) == prefix
+    assert pool.free_blocks == free and pool.table("hit") == prefix
+    assert [pool.refcount(p) for p in prefix] == [3, 3]
+    with pytest.raises(ValueError, match="already owns"):
+        pool.attach("hit", prefix)
+    with pytest.raises(ValueError, match="attached pages must be distinct"):
+        pool.attach("dup", [prefix[0], prefix[0]])
+    with pytest.raises(ValueError, match="cannot attach unallocated block: 7"):
+        pool.attach("dead", [prefix[0], 7])
+    assert pool.refcount(prefix[0]) == 3  # a refused attach takes no reference
+    pool.free("prefix")
+    pool.free("hit")
+    assert [pool.refcount(p) for p in prefix] == [1, 1] and pool.free_blocks == free
+    pool.unpin(prefix)
+    assert pool.free_blocks == 8
+    with pytest.raises(ValueError, match="cannot attach unallocated block"):
+        pool.attach("late", prefix)
+
+
 def test_fused_norm_rope_write_checks_before_any_launch():
     from mini_engine_hip.kernels.rope import qk_norm_rope_write_kv
     q, key, value, *_ = inputs()
