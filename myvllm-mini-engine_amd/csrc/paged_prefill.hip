@@ -95,7 +95,7 @@ struct PrefillArgs {
     int q_heads;
     int kv_heads;
     int group;
-    int qb;        // query tokens per item (kPfRows / group)
+    int qb;        // query tokens per item (kPfRows / group, rounded down)
     int chunk;     // keys per item (multiple of kPfKeys)
     int max_chunks;
     int chunk_choice;  // 1: a walk with more than one round of items may take a larger chunk
@@ -444,15 +444,20 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     const int t_begin = chunk_start / kPfKeys;
     const int t_end = chunk_end > chunk_start ? (chunk_end + kPfKeys - 1) / kPfKeys : t_begin;
 
-    // The kPfNb 16-row column blocks of this wave.
+    // The kPfNb 16-row column blocks of this wave.  Row r is token r % qb of
+    // the block and head r / qb of the group; when the group does not divide
+    // kPfRows the rows from qb * group on are idle (placed past the block's
+    // tokens, so nothing reads or writes for them).
     int qi[kPfNb], head[kPfNb], pos[kPfNb];
     bool row_ok[kPfNb];
     int wave_last = -1, wave_first = 0x7fffffff;
+    const int rows_used = a.qb * a.group;
 #pragma unroll
     for (int nb = 0; nb < kPfNb; ++nb) {
         const int r = wave * (16 * kPfNb) + nb * 16 + li;
-        qi[nb] = q0 + r % a.qb;
-        head[nb] = kvh * a.group + r / a.qb;
+        const bool in_block = r < rows_used;
+        qi[nb] = in_block ? q0 + r % a.qb : qlen;
+        head[nb] = kvh * a.group + (in_block ? r / a.qb : 0);
         const int64_t p64 = (int64_t)start + qi[nb];
         row_ok[nb] = qi[nb] < qlen && start >= 0 && p64 < ctx && p64 < cap;
         pos[nb] = (int)p64;
@@ -1269,7 +1274,7 @@ PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_
                               int64_t head_dim, int64_t block_size, int64_t table_width, int64_t chunk_tokens) {
     PrefillPlan p{};
     const int64_t group = q_heads / kv_heads;
-    p.mfma = head_dim == kPfD && kPfRows % group == 0;
+    p.mfma = head_dim == kPfD && group <= kPfRows;
     if (!p.mfma) return p;
     p.qb = (int)(kPfRows / group);
     const int64_t cap = table_width * block_size;

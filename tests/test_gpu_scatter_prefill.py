@@ -217,6 +217,33 @@ def test_mfma_prefill_gqa_groups(group, heads):
     assert max_err(actual, expected) <= GATE[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("group,heads,chunk_tokens", [
+    (3, 24, 0), (5, 40, 256), (7, 28, 0), (7, 28, 192), (6, 12, 320), (40, 40, 0), (100, 100, 256),
+])
+def test_mfma_prefill_groups_not_dividing_the_row_block(dtype, group, heads, chunk_tokens):
+    """Groups that do not divide the 256 rows of a query block (Qwen-family
+    layouts such as 28/4 and 40/8 heads): the block holds 256 // group tokens
+    and its last 256 % group rows are idle.  Every head of every token is
+    checked, so an idle row that wrote into the next kv head's output would
+    fail, with and without a key split (the merge then reads the partials)."""
+    gen = torch.Generator().manual_seed(1000 + group)
+    kv_heads = heads // group
+    block, pages, width = 16, 200, 90
+    kc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
+    vc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
+    tables = torch.randperm(pages, generator=gen)[:2 * width].view(2, width)
+    cu = torch.tensor([0, 150, 227])
+    starts = torch.tensor([1200, 41])
+    lens = starts + (cu[1:] - cu[:-1])
+    q = torch.randn(227, heads, 128, generator=gen).to(dtype)
+    args = [q, kc, vc, cu, starts, tables, lens]
+    print(f"prefill group={group} heads={heads} chunk={chunk_tokens} {dtype}", flush=True)
+    actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip", chunk_tokens=chunk_tokens)
+    expected = paged_oracle.paged_prefill_attention(*args, block, cast=False)
+    assert max_err(actual, expected) <= GATE[dtype]
+
+
 def test_c5_chunked_prefill_full_size():
     """8 sequences x 128 new tokens after U[0,3968] prior tokens, block 256, bf16."""
     case = workloads.chunked_prefill_case(device=DEV)
