@@ -405,11 +405,16 @@ __device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, in
 }
 
 
-// One work item, computed by the whole work-group.
-template <typename T, int PAGES>
+// One work item, computed by the whole work-group.  NARROW: head_dim is a
+// multiple of 8 below kPfD; rows are zero-padded to kPfD in LDS (the copies
+// skip the padded 16-byte chunks, which stay zero), the queries' padded dims
+// are zero, and only head_dim output dims are stored.
+template <typename T, int PAGES, bool NARROW>
 __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a, const PrefillItem& item,
                                                             PrefillLds& lds) {
     constexpr bool SCALAR_PAGES = PAGES != kPagesPerLane;
+    const int hd = NARROW ? a.head_dim : kPfD;  // elements per K/V/Q/output row in memory
+    const int dchunks = hd / 8;                 // 16-byte chunks per row
     auto& sm_k = lds.k;
     auto& sm_v = lds.v;
     auto& sm_b = lds.b;
@@ -516,18 +521,22 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     // instructions j = kPfIpw*w + i, each covering key rows 4j..4j+3 (lane ->
     // row 4j + lane/16, LDS slot lane%16 = global chunk (lane%16)^(row&15) for
     // K, (lane%16)^(2*row&15) for V).
-    const int64_t row_bytes_g = (int64_t)a.kv_heads * kPfD * 2;
+    const int64_t row_bytes_g = (int64_t)a.kv_heads * hd * 2;
     const int64_t page_bytes_g = (int64_t)a.block_size * row_bytes_g;
-    const uint8_t* kcache = static_cast<const uint8_t*>(a.key_cache) + (int64_t)kvh * kPfD * 2;
-    const uint8_t* vcache = static_cast<const uint8_t*>(a.value_cache) + (int64_t)kvh * kPfD * 2;
+    const uint8_t* kcache = static_cast<const uint8_t*>(a.key_cache) + (int64_t)kvh * hd * 2;
+    const uint8_t* vcache = static_cast<const uint8_t*>(a.value_cache) + (int64_t)kvh * hd * 2;
     const int bs_shift = a.block_shift;
     const int lrow = lane >> 4;  // row inside the instruction's 4 rows
     uint32_t tile_off[kPfIpw], tile_off_v[kPfIpw];  // per-lane byte offsets of whole-tile copies from row 0
+    bool kchunk_ok[kPfIpw], vchunk_ok[kPfIpw];      // the lane's global chunk lies inside the row
 #pragma unroll
     for (int i = 0; i < kPfIpw; ++i) {
         const int row = 4 * (kPfIpw * wave + i) + lrow;
-        tile_off[i] = (uint32_t)(row * row_bytes_g) + 16u * (uint32_t)((lane & 15) ^ (row & 15));
-        tile_off_v[i] = (uint32_t)(row * row_bytes_g) + 16u * (uint32_t)((lane & 15) ^ ((2 * row) & 15));
+        const int kc = (lane & 15) ^ (row & 15), vc = (lane & 15) ^ ((2 * row) & 15);
+        kchunk_ok[i] = !NARROW || kc < dchunks;
+        vchunk_ok[i] = !NARROW || vc < dchunks;
+        tile_off[i] = (uint32_t)(row * row_bytes_g) + 16u * (uint32_t)(kchunk_ok[i] ? kc : 0);
+        tile_off_v[i] = (uint32_t)(row * row_bytes_g) + 16u * (uint32_t)(vchunk_ok[i] ? vc : 0);
     }
 
     // The table is read-only here: reading it through the constant address
@@ -592,8 +601,8 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 #pragma unroll
                 for (int i = 0; i < kPfIpw; ++i) {
                     const int j = kPfIpw * wave + i;
-                    lds_dma16_s(kcache + base, tile_off[i], lk + 1024 * j);
-                    lds_dma16_s(vcache + base, tile_off_v[i], lv + 1024 * j);
+                    if (kchunk_ok[i]) lds_dma16_s(kcache + base, tile_off[i], lk + 1024 * j);
+                    if (vchunk_ok[i]) lds_dma16_s(vcache + base, tile_off_v[i], lv + 1024 * j);
                 }
                 return;
             }
@@ -615,8 +624,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             if (ok) {
                 const int in_page = bs_shift >= 0 ? key & (a.block_size - 1) : key % a.block_size;
                 const int64_t off = (int64_t)page * page_bytes_g + (int64_t)in_page * row_bytes_g;
-                gk = kcache + off + 16 * cidx;
-                gv = vcache + off + 16 * cidx_v;
+                // Padded chunks of narrow rows copy zeros.
+                if (!NARROW || cidx < dchunks) gk = kcache + off + 16 * cidx;
+                if (!NARROW || cidx_v < dchunks) gv = vcache + off + 16 * cidx_v;
             }
             lds_dma16(gk, lds_addr(&sm_k[st][0]) + 1024 * j);
             lds_dma16(gv, lds_addr(&sm_v[st][0]) + 1024 * j);
@@ -632,11 +642,12 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     u32x4 qop[kPfNb][4];
 #pragma unroll
     for (int nb = 0; nb < kPfNb; ++nb) {
-        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + ((row0 + qi[nb]) * a.q_heads + head[nb]) * kPfD;
+        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + ((row0 + qi[nb]) * a.q_heads + head[nb]) * hd;
 #pragma unroll
         for (int dc = 0; dc < 4; ++dc) {
             qop[nb][dc] = u32x4{0u, 0u, 0u, 0u};
-            if (row_ok[nb]) qop[nb][dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
+            if (row_ok[nb] && (!NARROW || 32 * dc + 8 * lg < hd))
+                qop[nb][dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
         }
     }
 
@@ -871,12 +882,12 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         const int64_t rowid = (row0 + qi[nb]) * a.q_heads + head[nb];
         if (nchunks == 1) {
             const float inv = (row_ok[nb] && l_row > 0.f) ? __builtin_amdgcn_rcpf(l_row) : 0.f;
-            uint16_t* orow = static_cast<uint16_t*>(a.out) + rowid * kPfD;
+            uint16_t* orow = static_cast<uint16_t*>(a.out) + rowid * hd;
 #pragma unroll
             for (int dt = 0; dt < 8; ++dt) {
                 const u32x2 w = {T::pack(o[nb][dt][0] * inv, o[nb][dt][1] * inv),
                                  T::pack(o[nb][dt][2] * inv, o[nb][dt][3] * inv)};
-                *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * lg) = w;
+                if (!NARROW || 16 * dt + 4 * lg < hd) *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * lg) = w;
             }
         } else {
             const int64_t slot = (int64_t)chunk * a.ws_rows + rowid;
@@ -995,13 +1006,22 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
 // true: one work-group per CU slot, each walking items idx, idx +
 // item_stride, ... below the item count (a separate instantiation, so that
 // the one-item kernel keeps its register allocation).
-template <typename T, int PAGES, bool WALK>
+template <typename T, int PAGES, bool WALK, bool NARROW>
 __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) PrefillLds lds;
+    if constexpr (NARROW && PAGES == kPagesPerTile) {
+        // Whole-tile copies skip the padded chunks of narrow rows: those LDS
+        // slots (the same in every stage and item) must hold zeros.
+        u32x4* ring = reinterpret_cast<u32x4*>(&lds.k[0][0]);
+        static_assert(offsetof(PrefillLds, v) == offsetof(PrefillLds, k) + sizeof(lds.k), "K and V rings adjacent");
+        constexpr int n16 = (int)(sizeof(lds.k) + sizeof(lds.v)) / 16;
+        for (int i = threadIdx.x; i < n16; i += kPfThreads) ring[i] = u32x4{0u, 0u, 0u, 0u};
+        __syncthreads();
+    }
     if constexpr (!WALK) {
         PrefillItem item;
         if (!find_item(a, a.chunk, blockIdx.x / a.kv_heads, item)) return;
-        prefill_item<T, PAGES>(a, item, lds);
+        prefill_item<T, PAGES, NARROW>(a, item, lds);
     } else {
         // The first lookup also counts the items, so that the walk ends
         // without a lookup past the end.
@@ -1035,7 +1055,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
             }
         }
         while (ok) {
-            prefill_item<T, PAGES>(a, item, lds);
+            prefill_item<T, PAGES, NARROW>(a, item, lds);
             idx += a.item_stride;
             if (idx >= total) break;
             __syncthreads();  // every wave is done with the LDS ring before the next item refills it
@@ -1049,7 +1069,8 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
 // chunks: with o_c the chunk's normalised output, l_c its probability sum and
 // m_c its reference, out = sum_c w_c o_c / sum_c w_c, w_c = l_c 2^(m_c - M).
 // One work-group per packed token (its chunk count comes from the attention
-// kernel); thread t handles head t/16, dims 8*(t%16) .. +8.
+// kernel); a thread handles 8 dims of one head.  Partial rows are kPfD wide
+// (heads narrower than kPfD are zero-padded there); the output has head_dim.
 constexpr int kMergeThreads = 256;
 
 template <typename T>
@@ -1060,9 +1081,10 @@ __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(Pref
     const int nchunks = min(a.ws_tok[token], a.max_chunks);
     if (nchunks <= 1) return;
     constexpr int kGroup = 8;  // chunks whose partials are loaded together
-    for (int idx = threadIdx.x; idx < a.q_heads * (kPfD / 8); idx += kMergeThreads) {
-        const int head = idx / (kPfD / 8);
-        const int d0 = 8 * (idx % (kPfD / 8));
+    const int dgroups = a.head_dim / 8;
+    for (int idx = threadIdx.x; idx < a.q_heads * dgroups; idx += kMergeThreads) {
+        const int head = idx / dgroups;
+        const int d0 = 8 * (idx - head * dgroups);
         const int64_t rowid = token * a.q_heads + head;  // chunk c's slot: c * ws_rows + rowid
         const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + rowid;
         // One pass: every load of a group of chunks is in flight together,
@@ -1126,7 +1148,7 @@ __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(Pref
         const float inv = sum > 0.f ? 1.f / sum : 0.f;
         const u32x4 wv = {T::pack(acc[0] * inv, acc[1] * inv), T::pack(acc[2] * inv, acc[3] * inv),
                           T::pack(acc[4] * inv, acc[5] * inv), T::pack(acc[6] * inv, acc[7] * inv)};
-        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + (token * a.q_heads + head) * kPfD + d0) = wv;
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + (token * a.q_heads + head) * a.head_dim + d0) = wv;
     }
 }
 
@@ -1256,6 +1278,7 @@ int check_prefill(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64
 
 struct PrefillPlan {
     bool mfma;
+    bool narrow;  // head_dim below kPfD, zero-padded in LDS
     int qb;
     int chunk;
     int max_chunks;
@@ -1274,7 +1297,10 @@ PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_
                               int64_t head_dim, int64_t block_size, int64_t table_width, int64_t chunk_tokens) {
     PrefillPlan p{};
     const int64_t group = q_heads / kv_heads;
-    p.mfma = head_dim == kPfD && group <= kPfRows;
+    // MFMA tiles for head_dim 128, and for narrower multiples of 8 padded to
+    // 128 in LDS (zero dims add nothing to the scores and give zero outputs).
+    p.narrow = head_dim < kPfD;
+    p.mfma = group <= kPfRows && (head_dim == kPfD || (head_dim % 8 == 0 && head_dim >= 8 && p.narrow));
     if (!p.mfma) return p;
     p.qb = (int)(kPfRows / group);
     const int64_t cap = table_width * block_size;
@@ -1412,35 +1438,37 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         const int64_t groups = item_slots * kv_heads;
         if (groups > 2147483647) return fail(MVME_EINVAL, "paged prefill grid too large");
         // Whole-tile pages need 32-bit per-lane offsets inside a tile.
-        const bool tile_pages = a.block_shift >= 6 && kv_heads * kPfD * 2 * kPfKeys < (int64_t(1) << 31);
-        const int pages = tile_pages ? kPagesPerTile : (block_size % 4 == 0 ? kPagesPerRows : kPagesPerLane);
+        const bool tile_pages = a.block_shift >= 6 && kv_heads * head_dim * 2 * kPfKeys < (int64_t(1) << 31);
+        int pages = tile_pages ? kPagesPerTile : (block_size % 4 == 0 ? kPagesPerRows : kPagesPerLane);
+        if (p.narrow && pages == kPagesPerRows) pages = kPagesPerLane;  // no narrow instantiation of that mode
         const dim3 grid((unsigned)groups), block(kPfThreads);
         auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, s, a); };
         auto launch_walk = [&](auto one, auto walk) {
             if (a.item_stride > 0) launch(walk);
             else launch(one);
         };
-        if (dtype == MVME_FP16) {
-            if (pages == kPagesPerTile)
-                launch_walk(paged_prefill_mfma_kernel<Half, kPagesPerTile, false>,
-                            paged_prefill_mfma_kernel<Half, kPagesPerTile, true>);
-            else if (pages == kPagesPerRows)
-                launch_walk(paged_prefill_mfma_kernel<Half, kPagesPerRows, false>,
-                            paged_prefill_mfma_kernel<Half, kPagesPerRows, true>);
-            else
-                launch_walk(paged_prefill_mfma_kernel<Half, kPagesPerLane, false>,
-                            paged_prefill_mfma_kernel<Half, kPagesPerLane, true>);
-        } else {
-            if (pages == kPagesPerTile)
-                launch_walk(paged_prefill_mfma_kernel<BFloat16, kPagesPerTile, false>,
-                            paged_prefill_mfma_kernel<BFloat16, kPagesPerTile, true>);
-            else if (pages == kPagesPerRows)
-                launch_walk(paged_prefill_mfma_kernel<BFloat16, kPagesPerRows, false>,
-                            paged_prefill_mfma_kernel<BFloat16, kPagesPerRows, true>);
-            else
-                launch_walk(paged_prefill_mfma_kernel<BFloat16, kPagesPerLane, false>,
-                            paged_prefill_mfma_kernel<BFloat16, kPagesPerLane, true>);
-        }
+        auto launch_type = [&](auto type_tag) {
+            using T = decltype(type_tag);
+            if (p.narrow) {
+                if (pages == kPagesPerTile)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true>);
+                else
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, true>,
+                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, true>);
+            } else if (pages == kPagesPerTile) {
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false>,
+                            paged_prefill_mfma_kernel<T, kPagesPerTile, true, false>);
+            } else if (pages == kPagesPerRows) {
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerRows, false, false>,
+                            paged_prefill_mfma_kernel<T, kPagesPerRows, true, false>);
+            } else {
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, false>,
+                            paged_prefill_mfma_kernel<T, kPagesPerLane, true, false>);
+            }
+        };
+        if (dtype == MVME_FP16) launch_type(Half{});
+        else launch_type(BFloat16{});
         if (p.max_chunks > 1) {
             const dim3 grid((unsigned)total_tokens);
             if (dtype == MVME_FP16)

@@ -244,6 +244,50 @@ def test_mfma_prefill_groups_not_dividing_the_row_block(dtype, group, heads, chu
     assert max_err(actual, expected) <= GATE[dtype]
 
 
+def _two_sequence_case(head_dim, heads, kv_heads, block, dtype, seed):
+    """Two sequences: 150 new tokens after 1200 cached, 77 after 41."""
+    gen = torch.Generator().manual_seed(seed)
+    cu = torch.tensor([0, 150, 227])
+    starts = torch.tensor([1200, 41])
+    lens = starts + (cu[1:] - cu[:-1])
+    width = -(-int(lens.max()) // block)
+    pages = 2 * width + 3
+    kc = torch.randn(pages, block, kv_heads, head_dim, generator=gen).to(dtype)
+    vc = torch.randn(pages, block, kv_heads, head_dim, generator=gen).to(dtype)
+    tables = torch.randperm(pages, generator=gen)[:2 * width].view(2, width)
+    q = torch.randn(227, heads, head_dim, generator=gen).to(dtype)
+    return [q, kc, vc, cu, starts, tables, lens]
+
+
+@pytest.mark.parametrize("head_dim,block,chunk_tokens,dtype,heads,kv_heads", [
+    (64, 256, 0, torch.bfloat16, 16, 8), (64, 256, 256, torch.float16, 16, 8), (8, 256, 0, torch.bfloat16, 8, 1),
+    (16, 16, 0, torch.float16, 4, 4), (40, 5, 0, torch.bfloat16, 16, 4), (72, 64, 192, torch.float16, 9, 3),
+    (96, 256, 192, torch.bfloat16, 28, 4), (120, 16, 320, torch.float16, 4, 2),
+])
+def test_mfma_prefill_narrow_heads(head_dim, block, chunk_tokens, dtype, heads, kv_heads):
+    """head_dim a multiple of 8 below 128 runs the MFMA kernel with rows
+    zero-padded to 128 in LDS: whole-tile copies (block 256, 64) skip the
+    padded chunks, per-row copies (block 16, 5) read zeros for them; with a
+    key split the partials are 128 wide and the merge writes head_dim."""
+    args = _two_sequence_case(head_dim, heads, kv_heads, block, dtype, seed=head_dim + block)
+    print(f"narrow prefill D={head_dim} block={block} chunk={chunk_tokens} {dtype} {heads}/{kv_heads}", flush=True)
+    actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip", chunk_tokens=chunk_tokens)
+    assert actual.shape == args[0].shape
+    assert max_err(actual, paged_oracle.paged_prefill_attention(*args, block, cast=False)) <= GATE[dtype]
+    assert max_err(actual, c_oracle.paged_prefill(*args, block)) <= GATE[dtype]
+
+
+@pytest.mark.parametrize("head_dim,block,dtype", [(100, 16, torch.bfloat16), (256, 256, torch.float16),
+                                                  (12, 4, torch.float16)])
+def test_generic_prefill_other_head_dims(head_dim, block, dtype):
+    """Head dims the MFMA kernel does not take (above 128, or not a multiple
+    of 8) run the one-wave-per-row kernel."""
+    args = _two_sequence_case(head_dim, 8, 4, block, dtype, seed=head_dim)
+    print(f"generic prefill D={head_dim} block={block} {dtype}", flush=True)
+    actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip")
+    assert max_err(actual, paged_oracle.paged_prefill_attention(*args, block, cast=False)) <= GATE[dtype]
+
+
 def test_c5_chunked_prefill_full_size():
     """8 sequences x 128 new tokens after U[0,3968] prior tokens, block 256, bf16."""
     case = workloads.chunked_prefill_case(device=DEV)
