@@ -165,11 +165,28 @@ def decode_step_with_scatter(args, torch, layers, write_kv_cache_batch, paged_at
                    "value_cache": c["value_cache"].cpu(), "block_tables": tables,
                    "context_lens": c["context_lens"].cpu()}
         err = max_abs(c["out"], cpu.decode(tensors, BLOCK))
+    # The same step with the write fused into the attention launch
+    # (paged_attention_decode_write): results equal the two launches bit for bit.
+    from mini_engine_hip.kernels.paged import paged_attention_decode_write
+    want = [c["out"].clone() for c in layers]
+    for c in layers:
+        c["out"].zero_()
+
+    def fused_step():
+        for c in layers:
+            paged_attention_decode_write(c["query"], c["key_cache"], c["value_cache"], c["block_tables"],
+                                         c["context_lens"], BLOCK, c["new_key"], c["new_value"], validate=False,
+                                         out=c["out"])
+
+    ms_fused, _ = graph_time_ms(fused_step, torch, calls_per_graph=LAYERS, replays=args.steps, warmup=args.warmup)
+    fused_equal = all(torch.equal(c["out"], w) for c, w in zip(layers, want))
     step_bytes = LAYERS * (layer_bytes() + 2 * BATCH * HKV * D * 2 * 2 + BATCH * 8)
     return {"us_per_step": ms * 1e3, "us_per_layer": ms * 1e3 / LAYERS,
             "TBps": step_bytes / (ms * 1e-3) / 1e12, "launches_per_step": 2 * LAYERS,
             "scatter_bit_exact": scatter_ok, "max_abs_error_layer0": err, "gate": 2e-3,
-            "passed": scatter_ok and (err is None or err <= 2e-3)}
+            "fused_write_us_per_layer": ms_fused * 1e3 / LAYERS, "fused_write_launches_per_step": LAYERS,
+            "fused_write_equals_two_launches": fused_equal,
+            "passed": scatter_ok and fused_equal and (err is None or err <= 2e-3)}
 
 
 def decode_attention_block_step(args, torch, layers, paged_attention, cpu):
@@ -229,12 +246,37 @@ def decode_attention_block_step(args, torch, layers, paged_attention, cpu):
         attn_err = max_abs(c["out"], cpu.decode(tensors, BLOCK))
         o_err = max_abs(c["hidden"], c["out"].float().cpu().view(BATCH, -1) @ c["w_o"].float().cpu().t())
         passed = v_exact and rope_err <= 4e-3 and attn_err <= 2e-3 and o_err <= 2e-2
+    # The same block with norm/RoPE and the KV write fused into the attention
+    # launch (paged_attention_decode_write), then o_proj: two launches per layer.
+    from mini_engine_hip.kernels.paged import paged_attention_decode_write
+    want = [(c["q_rot"].clone(), c["out"].clone(), c["hidden"].clone()) for c in layers]
+    for c in layers:
+        c["q_rot"].zero_()
+        c["out"].zero_()
+        c["hidden"].zero_()
+
+    def fused_step():
+        for c in layers:
+            q, k, v = split(c)
+            paged_attention_decode_write(q, c["key_cache"], c["value_cache"], c["block_tables"], c["context_lens"],
+                                         BLOCK, k, v, q_weight=c["wq"], k_weight=c["wk"], cos=c["cos"],
+                                         sin=c["sin"], q_out=c["q_rot"], validate=False, out=c["out"])
+            linear_rows(c["out"].view(BATCH, HQ * D), c["w_o"], out=c["hidden"])
+
+    ms_fused, _ = graph_time_ms(fused_step, torch, calls_per_graph=2 * LAYERS, replays=args.steps,
+                                warmup=args.warmup)
+    fused_equal = all(torch.equal(c["q_rot"], w[0]) and torch.equal(c["out"], w[1]) and torch.equal(c["hidden"], w[2])
+                      for c, w in zip(layers, want))
+    if passed is not None:
+        passed = passed and fused_equal
     for c in layers:
         for key in ("qkv", "wq", "wk", "cos", "sin", "w_o", "positions", "q_rot", "hidden"):
             del c[key]
     return {"us_per_step": ms * 1e3, "us_per_layer": ms * 1e3 / LAYERS, "launches_per_step": 3 * LAYERS,
             "v_rows_bit_exact": v_exact, "max_abs_error_rope_layer0": rope_err,
-            "max_abs_error_attention_layer0": attn_err, "max_abs_error_o_proj_layer0": o_err, "passed": passed}
+            "max_abs_error_attention_layer0": attn_err, "max_abs_error_o_proj_layer0": o_err,
+            "fused_prologue_us_per_layer": ms_fused * 1e3 / LAYERS, "fused_prologue_launches_per_step": 2 * LAYERS,
+            "fused_prologue_equals_three_launches": fused_equal, "passed": passed}
 
 
 def _median_seconds(fn, budget_s, min_runs=5, max_runs=20):

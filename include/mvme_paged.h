@@ -168,6 +168,45 @@ int mvme_paged_attention_noalloc(void* out, const void* query,
                                  int64_t partition_tokens, int dtype, void* stream);
 
 /*
+ * The decode step's KV write and paged attention in one launch.  Before
+ * attention, every sequence b's new token -- at position context_lens[b] - 1
+ * -- is written into the cache:
+ *   q_weight == NULL: key_cache / value_cache row = new_key / new_value row
+ *     (the decode-batch KV write), and `query` is the attention query
+ *     ([batch, q_heads, head_dim], contiguous);
+ *   q_weight != NULL: the K row is rope(rmsnorm(new_key, k_weight), cos, sin)
+ *     and the V row new_value, and the attention query is
+ *     rope(rmsnorm(query, q_weight), cos, sin) of the raw query rows
+ *     (query_token_stride elements apart); the rotated queries also go to
+ *     q_out ([batch, q_heads, head_dim]) when it is not NULL.  cos / sin are
+ *     [batch, head_dim / 2] at each sequence's position; eps the RMSNorm eps.
+ * Then attention over context_lens[b] tokens exactly as mvme_paged_attention
+ * (same workspace).  Results equal the two-launch sequence
+ * (mvme_write_kv_cache_batch, or mvme_qk_norm_rope_write_kv in decode mode,
+ * then mvme_paged_attention) bit for bit: the norm/RoPE arithmetic is the
+ * same code.  A new token whose page is absent or out of range is not
+ * written.  new_key / new_value are [batch, kv_heads, head_dim] rows,
+ * key_token_stride / value_token_stride elements apart.  head_dim 16, 32,
+ * 64, 128 or 256; every row 16-byte aligned.
+ * Fuses what the reference runs as separate launches in
+ * Attention.forward_decode_batch (mini_engine/model/native_qwen3.py:179-197):
+ * q/k RMSNorm (elementwise.cu norm kernel), RoPE (data.cu:29-65), the batch
+ * KV write (data.cu:88-107) and paged_attention (paged_attention.cu:52-280).
+ * No single counterpart in the reference.
+ */
+int mvme_paged_attention_decode_write(void* out, const void* query, void* key_cache, void* value_cache,
+                                      const int64_t* block_tables, const int64_t* context_lens,
+                                      int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                      int64_t num_blocks, int64_t block_size, int64_t table_width,
+                                      int64_t partition_tokens, int dtype,
+                                      const void* new_key, const void* new_value,
+                                      int64_t key_token_stride, int64_t value_token_stride,
+                                      const void* q_weight, const void* k_weight,
+                                      const void* cos, const void* sin, float eps,
+                                      int64_t query_token_stride, void* q_out,
+                                      void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Bytes of device workspace mvme_paged_prefill_attention needs for these
  * shapes and element type (0 when no query block is split over key chunks).
  * Pure host function.  chunk_tokens: 0 selects the library's default key

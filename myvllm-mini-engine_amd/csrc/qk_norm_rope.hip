@@ -18,7 +18,7 @@
 // (p, p + D/2) for p = lane, lane + 64, ..., so the rotation never leaves the
 // lane).  Rows whose slot is out of range skip the cache write (q_out is
 // always written).
-#include "mvme_common.h"
+#include "norm_rope.h"
 
 namespace mvme {
 namespace {
@@ -59,16 +59,6 @@ __device__ inline int64_t rope_slot(const RopeArgs& a, int64_t t) {
     const int64_t page = a.tables[t * a.table_width + pos / a.block_size];
     if (page < 0 || page >= a.num_blocks) return -1;
     return page * a.block_size + pos % a.block_size;
-}
-
-template <typename T>
-__device__ inline float to_f(uint16_t h) {
-    return T::lo((uint32_t)h);
-}
-
-template <typename T>
-__device__ inline float round_t(float x) {
-    return to_f<T>(T::from_float(x));
 }
 
 // RMSNorm + RoPE of one head row `src` (dim elements) into `dst`.
@@ -186,44 +176,7 @@ __global__ __launch_bounds__(kVecThreads) void qk_norm_rope_vec_kernel(RopeArgs 
     // loads, so that their latencies overlap instead of adding up.
     const int64_t slot = live && !is_q ? rope_slot(a, t) : -1;
 
-    float x[8];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        x[2 * j] = T::lo(xv[j]);
-        x[2 * j + 1] = T::hi(xv[j]);
-    }
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss = fmaf(x[j], x[j], ss);
-    ss = group_sum<L>(ss);
-    const float inv = 1.f / sqrtf(ss / (float)kDim + a.eps);
-    float n[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        float m = x[j] * inv;  // fp32 rounding, then T (see norm_rope_row)
-        asm volatile("" : "+v"(m));
-        const float wj = (j & 1) ? T::hi(wv[j / 2]) : T::lo(wv[j / 2]);
-        n[j] = round_t<T>(round_t<T>(m) * wj);
-    }
-    const bool first = sub < kHalfLanes;
-    u32x4 out;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t mine = T::pack(n[2 * j], n[2 * j + 1]);
-        const uint32_t other = (uint32_t)__builtin_amdgcn_ds_bpermute((__lane_id() ^ kHalfLanes) << 2, (int)mine);
-        float o[2];
-#pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const float own = n[2 * j + e];
-            const float partner = e ? T::hi(other) : T::lo(other);
-            const float c = e ? T::hi(cv[j]) : T::lo(cv[j]);
-            const float s = e ? T::hi(sv[j]) : T::lo(sv[j]);
-            // first half: x1*c - x2*s with x1 = own; second half: x1*s + x2*c with x1 = partner.
-            o[e] = first ? round_t<T>(round_t<T>(own * c) - round_t<T>(partner * s))
-                         : round_t<T>(round_t<T>(partner * s) + round_t<T>(own * c));
-        }
-        out[j] = T::pack(o[0], o[1]);
-    }
+    const u32x4 out = norm_rope_lanes<T, L>(xv, wv, cv, sv, a.eps, sub);
     if (!live) return;
     const int64_t cache_row = slot * (int64_t)a.kv_heads * kDim + (int64_t)h * kDim + sub * 8;
     if (is_q) {

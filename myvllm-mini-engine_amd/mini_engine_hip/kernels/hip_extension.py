@@ -37,6 +37,9 @@ SIGNATURES = {
                                     _i64, _i64, _int, _vp, _size, _vp]),
     "mvme_paged_attention_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _int, _vp]),
+    "mvme_paged_attention_decode_write": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                                 _i64, _i64, _i64, _int, _vp, _vp, _i64, _i64, _vp, _vp, _vp,
+                                                 _vp, ctypes.c_float, _i64, _vp, _vp, _size, _vp]),
     "mvme_paged_prefill_workspace_size": (_size, [_i64] * 8 + [_int]),
     "mvme_paged_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _size, _vp]),

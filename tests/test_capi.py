@@ -30,7 +30,7 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     symbols = declared_symbols()
-    assert len(symbols) == 15
+    assert len(symbols) == 16
     raw = ctypes.CDLL(str(hip_build.library_path()))
     for name in symbols:
         assert hasattr(raw, name), name
@@ -96,6 +96,29 @@ def test_noalloc_decode_rejects_before_touching_the_device(lib):
     assert "8388608" in lib.last_error() and "no-alloc" in lib.last_error()
     assert call(2, 16, 0, dtype=7) == ext.EINVAL and "FP16/BF16" in lib.last_error()
     assert call(2, 16, 0, out=None) == ext.EINVAL and "null pointer" in lib.last_error()
+
+
+def test_decode_write_rejects_before_touching_the_device(lib):
+    """The fused KV-write decode entry checks shapes, pointers, head_dim,
+    norm inputs, strides and alignment before any HIP call."""
+    def call(head_dim=128, q_weight=None, k_weight=None, cos=None, sin=None, eps=1e-6, k_stride=None,
+             q_stride=None, ptr=256, new_k=256):
+        k_stride = 8 * head_dim if k_stride is None else k_stride
+        q_stride = 16 * head_dim if q_stride is None else q_stride
+        return _status(lib, "mvme_paged_attention_decode_write", ptr, ptr, ptr, ptr, ptr, ptr, 2, 16, 8, head_dim,
+                       4, 16, 2, 0, 0, new_k, ptr, k_stride, 8 * head_dim, q_weight, k_weight, cos, sin, eps,
+                       q_stride, None, None, 0, None)
+
+    assert call(head_dim=80) == ext.EINVAL and "16,32,64,128,256" in lib.last_error()
+    assert call(new_k=None) == ext.EINVAL and "null pointer" in lib.last_error()
+    assert call(q_weight=256) == ext.EINVAL and "q_weight, k_weight, cos and sin" in lib.last_error()
+    assert call(q_weight=256, k_weight=256, cos=256, sin=256, eps=0.0) == ext.EINVAL
+    assert "eps" in lib.last_error()
+    assert call(k_stride=100) == ext.EINVAL and "stride" in lib.last_error()
+    assert call(q_weight=256, k_weight=256, cos=256, sin=256, q_stride=1000) == ext.EINVAL
+    assert "stride" in lib.last_error()
+    assert call(ptr=258) == ext.EINVAL and "16-byte aligned" in lib.last_error()
+    assert call(k_stride=8 * 128 + 4) == ext.EINVAL and "16-byte aligned" in lib.last_error()
 
 
 def test_scatter_and_prefill_reject_bad_arguments(lib):
