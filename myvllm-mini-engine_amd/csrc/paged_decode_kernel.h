@@ -21,9 +21,9 @@
 // each work-group writes its sequence's new token -- at position len - 1 --
 // into the kv head's cache row, either as given (the decode-batch KV write)
 // or after per-head RMSNorm + RoPE of k, with the query heads of its tile
-// normalised and rotated the same way into LDS.  The rows are written by
-// every work-group whose token range holds the position (identical bytes
-// from each G-tile) and read back by the same work-group after a barrier.
+// normalised and rotated the same way.  The row is written by the one wave
+// that later reads that position (in every work-group whose token range
+// holds it: identical bytes from each G-tile), so no barrier is needed.
 //
 // Scores: packed dot2 (fp16/bf16 products, fp32 accumulation) on the lane's
 // 8 elements, then a DPP reduction across the LPT lanes of the token.
@@ -192,70 +192,66 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     // row 0 the kv head's new K (and V), rows 1 .. G the tile's query heads
     // (mode 2) -- one row per kLpt lanes.
     static_assert(!PRO || (S::kLpt == S::kChunks && S::kLpt >= 2), "prologue needs head_dim 16/32/64/128/256");
-    __shared__ __attribute__((aligned(16))) uint16_t sm_q[PRO ? G : 1][PRO ? D : 8];
+    // Fused prologue, with no barrier: the wave whose iterations hold the new
+    // position writes its K/V row (and waits for that store before it loads
+    // the row again); in mode 2 every wave rotates the tile's query rows
+    // itself, into its own slice of LDS.  One row per kLpt lanes.
+    __shared__ __attribute__((aligned(16))) uint16_t sm_q[PRO ? NW : 1][PRO ? G : 1][PRO ? D : 8];
+    const int pos = len - 1;
+    // Token t is read by wave ((t - start) / kTpi) mod NW.
+    const bool owner = PRO && pos >= start && pos < end && ((pos - start) / S::kTpi) % NW == wave;
     if constexpr (PRO) {
-        {
-            const int pos = len - 1;
-            int64_t slot = -1;
-            if (pos >= start && pos < end) {
-                const int64_t page = a.tables[(int64_t)b * a.table_width +
-                                              (a.block_shift >= 0 ? pos >> a.block_shift : pos / a.block_size)];
-                if (page >= 0 && page < a.num_blocks)
-                    slot = page * a.block_size + (a.block_shift >= 0 ? pos & (a.block_size - 1) : pos % a.block_size);
+        int64_t slot = -1;
+        if (owner) {
+            const int64_t page = a.tables[(int64_t)b * a.table_width +
+                                          (a.block_shift >= 0 ? pos >> a.block_shift : pos / a.block_size)];
+            if (page >= 0 && page < a.num_blocks)
+                slot = page * a.block_size + (a.block_shift >= 0 ? pos & (a.block_size - 1) : pos % a.block_size);
+        }
+        const int64_t cache_row = slot * a.kv_heads * D + (int64_t)kvh * D + 8 * c;
+        const uint16_t* kv_src = a.new_k + (int64_t)b * a.k_stride + kvh * D + 8 * c;
+        const uint16_t* v_src = a.new_v + (int64_t)b * a.v_stride + kvh * D + 8 * c;
+        uint16_t* kdst = static_cast<uint16_t*>(const_cast<void*>(a.key_cache)) + cache_row;
+        uint16_t* vdst = static_cast<uint16_t*>(const_cast<void*>(a.value_cache)) + cache_row;
+        if (a.prologue == 1) {
+            if (slot >= 0 && tl == 0) {
+                const u32x4 kx = *reinterpret_cast<const u32x4*>(kv_src);
+                const u32x4 vx = *reinterpret_cast<const u32x4*>(v_src);
+                *reinterpret_cast<u32x4*>(kdst) = kx;
+                *reinterpret_cast<u32x4*>(vdst) = vx;
             }
+        } else {
+            // Rows 0 .. G-1: the tile's query heads; row G (owner only): the new K.
             constexpr int kRowsPerWave = kWave / S::kLpt;
-            const int rows = a.prologue == 2 ? G + 1 : 1;
-            const int64_t cache_row = slot * a.kv_heads * D + (int64_t)kvh * D + 8 * c;
-            for (int r0 = wave * kRowsPerWave; r0 < rows; r0 += NW * kRowsPerWave) {
+            const int rows = G + (slot >= 0 ? 1 : 0);
+            for (int r0 = 0; r0 < rows; r0 += kRowsPerWave) {
                 const int row = r0 + tl;
                 const bool live = row < rows;
-                const uint16_t* kv_src = a.new_k + (int64_t)b * a.k_stride + kvh * D + 8 * c;
-                if (a.prologue == 1) {
-                    if (row == 0 && slot >= 0) {
-                        const u32x4 kx = *reinterpret_cast<const u32x4*>(kv_src);
-                        const u32x4 vx = *reinterpret_cast<const u32x4*>(a.new_v + (int64_t)b * a.v_stride +
-                                                                       kvh * D + 8 * c);
-                        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(const_cast<void*>(a.key_cache)) +
-                                                  cache_row) = kx;
-                        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(const_cast<void*>(a.value_cache)) +
-                                                  cache_row) = vx;
-                    }
-                    continue;
-                }
+                const bool is_k = row == G;
                 // Lanes past the list compute on zeros and store nothing (the
                 // sum of squares and the rotation exchange read every lane).
-                const uint16_t* src = row == 0 ? kv_src
-                                               : static_cast<const uint16_t*>(a.query) + (int64_t)b * a.q_stride +
-                                                     (int64_t)(h0 + (live ? row - 1 : 0)) * D + 8 * c;
+                const uint16_t* src = is_k ? kv_src
+                                           : static_cast<const uint16_t*>(a.query) + (int64_t)b * a.q_stride +
+                                                 (int64_t)(h0 + (live ? row : 0)) * D + 8 * c;
                 const u32x4 zero = {0u, 0u, 0u, 0u};
                 const u32x4 xraw = *reinterpret_cast<const u32x4*>(src);
                 const u32x4 xv = live ? xraw : zero;
-                const u32x4 wv = *reinterpret_cast<const u32x4*>((row == 0 ? a.k_weight : a.q_weight) + 8 * c);
+                const u32x4 wv = *reinterpret_cast<const u32x4*>((is_k ? a.k_weight : a.q_weight) + 8 * c);
                 const int64_t trig = (int64_t)b * (D / 2) + (c % (S::kLpt / 2)) * 8;
                 const u32x4 cv = *reinterpret_cast<const u32x4*>(a.cos + trig);
                 const u32x4 sv = *reinterpret_cast<const u32x4*>(a.sin + trig);
                 const u32x4 rot = norm_rope_lanes<T, S::kLpt>(xv, wv, cv, sv, a.eps, c);
                 if (!live) continue;
-                if (row == 0) {
-                    if (slot >= 0) {
-                        const u32x4 vx = *reinterpret_cast<const u32x4*>(a.new_v + (int64_t)b * a.v_stride +
-                                                                       kvh * D + 8 * c);
-                        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(const_cast<void*>(a.key_cache)) +
-                                                  cache_row) = rot;
-                        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(const_cast<void*>(a.value_cache)) +
-                                                  cache_row) = vx;
-                    }
+                if (is_k) {
+                    const u32x4 vx = *reinterpret_cast<const u32x4*>(v_src);
+                    *reinterpret_cast<u32x4*>(kdst) = rot;
+                    *reinterpret_cast<u32x4*>(vdst) = vx;
                 } else {
-                    *reinterpret_cast<u32x4*>(&sm_q[row - 1][8 * c]) = rot;
-                    if (a.q_out && part == 0)
-                        *reinterpret_cast<u32x4*>(a.q_out + ((int64_t)b * a.q_heads + h0 + row - 1) * D + 8 * c) =
-                            rot;
+                    *reinterpret_cast<u32x4*>(&sm_q[wave][row][8 * c]) = rot;
+                    if (a.q_out && part == 0 && wave == 0)
+                        *reinterpret_cast<u32x4*>(a.q_out + ((int64_t)b * a.q_heads + h0 + row) * D + 8 * c) = rot;
                 }
             }
-            // The rows written above are read back below by other waves of
-            // this work-group: every store completes before the barrier.
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
         }
     }
 
@@ -265,7 +261,7 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     for (int g = 0; g < G; ++g) {
         u32x4 w = {0u, 0u, 0u, 0u};
         if (PRO && a.prologue == 2) {
-            if (chunk_ok) w = *reinterpret_cast<const u32x4*>(&sm_q[PRO ? g : 0][PRO ? 8 * c : 0]);
+            if (chunk_ok) w = *reinterpret_cast<const u32x4*>(&sm_q[PRO ? wave : 0][PRO ? g : 0][PRO ? 8 * c : 0]);
         } else if (chunk_ok)
             w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.query) +
                                                 ((int64_t)b * a.q_heads + h0 + g) * D + 8 * c);
@@ -308,6 +304,9 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     for (; it < end; it += kStep) {
         u32x4 kk[L], vv[L];
         bool ok[L];
+        // The owner's store of the new row completes before the row is read.
+        if constexpr (PRO)
+            if (owner && it <= pos && pos < it + S::kTpi) __builtin_amdgcn_s_waitcnt(0);
         if constexpr (PAGE_UNIFORM) {
             const int64_t page = page_next;
             page_next = page_of(it + kStep);
