@@ -5,7 +5,8 @@ Restates the capture/replay contract of the reference's decode graph bucket
 hip path, without the model around it: per layer the new token's K/V write
 (``write_kv_cache_batch``, or the fused q/k RMSNorm + RoPE + KV write in
 decode mode), then paged attention over ``positions + 1`` tokens — the order
-of Attention.forward_decode_batch (mini_engine/model/native_qwen3.py:179-197).
+of Attention.forward_decode_batch (mini_engine/model/native_qwen3.py:179-197)
+— or all of it in one launch (``paged_attention_decode_write``).
 
 The bucket has a fixed batch; rows past the active count are padding rows
 that decode position 0 through a private reserved page (column 0 of their
@@ -28,7 +29,7 @@ import torch
 from gpu_cases import assert_rope_close
 from mini_engine_hip.cache.kv_cache import KVCachePool
 from mini_engine_hip.kernels.data import write_kv_cache_batch
-from mini_engine_hip.kernels.paged import paged_attention
+from mini_engine_hip.kernels.paged import paged_attention, paged_attention_decode_write
 from mini_engine_hip.kernels.rope import qk_norm_rope_write_kv
 from oracle import paged_oracle
 
@@ -72,6 +73,13 @@ class DecodeBucket:
                 write_kv_cache_batch(key_pages, value_pages, self.tables, self.positions, self.k[layer],
                                      self.v[layer], BLOCK, backend="hip", validate=False)
                 query = self.q[layer]
+            elif self.mode == "decode_write":
+                # Norm/RoPE, KV write and attention in one launch.
+                paged_attention_decode_write(self.q[layer], key_pages, value_pages, self.tables, lengths, BLOCK,
+                                             self.k[layer], self.v[layer], q_weight=self.wq, k_weight=self.wk,
+                                             cos=self.cos, sin=self.sin, q_out=self.q_rot[layer], validate=False,
+                                             out=self.out[layer])
+                continue
             else:
                 query = qk_norm_rope_write_kv(self.q[layer], self.k[layer], self.v[layer], self.wq, self.wk,
                                               self.cos, self.sin, key_pages, value_pages,
@@ -136,7 +144,7 @@ def expected_after(bucket, before_k, before_v, host_pos, host_tables):
     return exp_k, exp_v, rot_q
 
 
-@pytest.mark.parametrize("mode", ["scatter", "fused"])
+@pytest.mark.parametrize("mode", ["scatter", "fused", "decode_write"])
 @pytest.mark.parametrize("dtype,width", [(torch.bfloat16, 6), (torch.float16, 80)])
 def test_decode_bucket_replays_with_new_metadata_and_padding(mode, dtype, width):
     """width 6 (96 tokens): whole-sequence decode; width 80 (1280 tokens, 8
@@ -180,7 +188,7 @@ def test_decode_bucket_replays_with_new_metadata_and_padding(mode, dtype, width)
         group = HQ // HKV
         for layer in range(LAYERS):
             q = rot_q[layer] if mode == "scatter" else got_q[layer]
-            if mode == "fused":
+            if mode != "scatter":
                 normed = paged_oracle.rms_norm(bucket.q[layer].cpu(), bucket.wq.cpu())
                 assert_rope_close(got_q[layer], rot_q[layer], normed, dtype)
             tensors = dict(zip(paged_oracle.TENSOR_NAMES, (q[:active], got_k[layer], got_v[layer],
@@ -200,5 +208,5 @@ def test_decode_bucket_replays_with_new_metadata_and_padding(mode, dtype, width)
         torch.cuda.synchronize()
         assert torch.equal(bucket.cache.key.cpu(), got_k) and torch.equal(bucket.cache.value.cpu(), got_v)
         assert torch.equal(bucket.out.cpu(), got_out)
-        if mode == "fused":
+        if mode != "scatter":
             assert torch.equal(bucket.q_rot.cpu(), got_q)
