@@ -445,10 +445,25 @@ def _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, cpu, dev,
         err = max_abs(out, cpu.decode({"query": c["query"].cpu(), "key_cache": kc, "value_cache": vc,
                                        "block_tables": c["block_tables"].cpu(),
                                        "context_lens": c["context_lens"].cpu()}, 16))
+    # The same step with the write inside the attention launch (the new token
+    # sits at position len - 1 = 511 of every sequence).
+    from mini_engine_hip.kernels.paged import paged_attention_decode_write
+    out_fused = torch.empty_like(out)
+
+    def fused(n=50):
+        def run():
+            for _ in range(n):
+                paged_attention_decode_write(c["query"], c["key_cache"], c["value_cache"], c["block_tables"],
+                                             c["context_lens"], 16, c["new_key"], c["new_value"], validate=False,
+                                             out=out_fused)
+        return run
+    ms_fused, _ = graph_time_ms(fused(), torch, calls_per_graph=50, replays=20, warmup=3)
     bytes_b8 = 8 * 512 * 4096 + 2 * 8 * 16 * 128 * 2 + 8 * 32 * 8 + 8 * 8
     extra["decode_b8_ctx512_bf16_with_scatter"] = {
         "us_per_call": ms / 50 * 1e3, "GBps_decode_bytes": bytes_b8 / (ms / 50 * 1e-3) / 1e9,
-        "scatter_bit_exact": bool(slots_ok), "max_abs_error": err, "reference_rtx5080_us": 40.340}
+        "scatter_bit_exact": bool(slots_ok), "max_abs_error": err, "reference_rtx5080_us": 40.340,
+        "fused_write_us_per_call": ms_fused / 50 * 1e3,
+        "fused_write_equals_two_launches": bool(torch.equal(out_fused, out))}
 
 
 def _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra):
