@@ -512,10 +512,15 @@ def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloa
     flops = workloads.prefill_flops(c["priors"])
     kv_bytes = sum(p + 128 for p in c["priors"]) * 4096 + 2 * 1024 * 16 * 128 * 2
     err = None if cpu is None else max_abs(holder["out"], cpu.prefill(*[a.cpu() for a in pargs], 256, cast=False))
+    # The call sits near the ridge point: its roofline time is the larger of
+    # the MFMA time and the HBM time of its algorithmic work.
+    bound_s = max(flops / (MFMA_BF16_PEAK_TFLOPS * 1e12), kv_bytes / (HBM_PEAK_GBS * 1e9))
     extra["chunked_prefill_8x128_bf16"] = {
         "us_per_call": per_call * 1e6, "TFLOPs": flops / per_call / 1e12,
         "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-        "GBps": kv_bytes / per_call / 1e9, "flops": flops, "priors": c["priors"],
+        "GBps": kv_bytes / per_call / 1e9, "frac_of_hbm_peak": kv_bytes / per_call / 1e9 / HBM_PEAK_GBS,
+        "algorithmic_bytes": kv_bytes, "roofline_bound_us": bound_s * 1e6,
+        "frac_of_roofline_time": bound_s / per_call, "flops": flops, "priors": c["priors"],
         "max_abs_error": err}
 
 
