@@ -167,3 +167,17 @@ def test_other_head_dims_run_two_launches():
     step = make_step(3, 8, 4, 80, 16, [20, 3, 57], torch.float16, seed=80)
     check_equal(step, 16, True)
     check_equal(step, 16, False, oracle=False)
+
+
+def test_trusted_empty_context_and_no_q_out():
+    """Trusted mode: a sequence with context length 0 writes nothing and
+    returns zeros (as the two launches do); norm/RoPE mode without q_out."""
+    step = make_step(3, 16, 8, 128, 16, [1, 5, 33], torch.bfloat16, seed=21)
+    step["lens"][0] = 0
+    want_k, want_v, _, want_out = two_launches(step, 16, True, 0, validate=False)
+    kc, vc = step["kc"].clone(), step["vc"].clone()
+    got = paged_attention_decode_write(step["q"], kc, vc, step["tables"], step["lens"], 16, step["k"], step["v"],
+                                       validate=False, **step["norm"])
+    torch.cuda.synchronize()
+    assert torch.equal(kc, want_k) and torch.equal(vc, want_v) and torch.equal(got, want_out)
+    assert not got[0].any()
