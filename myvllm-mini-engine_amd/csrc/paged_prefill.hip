@@ -69,6 +69,27 @@ constexpr int kPfD = 128;
 constexpr int kRowBytes = kPfD * 2;             // 256-byte key row
 constexpr int kTileBytes = kPfKeys * kRowBytes;  // 16 KiB per K or V tile
 
+// Tile shape of the MFMA kernel by padded head dim: 128 (head_dim 128 and
+// narrower multiples of 8) or 256.  Every tile is 16 KiB of K (and of V) in
+// LDS; at 256 a wave holds one 16-row block (the accumulators of 256 dims
+// fill the registers two blocks used) and a tile has 32 keys.
+template <int HD>
+struct PfShape {
+    static_assert(HD == 128 || HD == 256, "padded head dim 128 or 256");
+    static constexpr int kD = HD;
+    static constexpr int kNb = HD == 128 ? 2 : 1;      // 16-row MFMA column blocks per wave
+    static constexpr int kRows = kPfWaves * kNb * 16;  // query rows per work-group
+    static constexpr int kKeys = HD == 128 ? 64 : 32;  // keys per LDS tile
+    static constexpr int kHalves = kKeys / 32;         // 32-key halves per tile
+    static constexpr int kRowBytes = HD * 2;           // bytes per K/V row in LDS
+    static constexpr int kChunks = HD / 8;             // 16-byte chunks per row
+    static constexpr int kRowsPerInst = 1024 / kRowBytes;  // rows per 1 KiB copy instruction
+    static constexpr int kIpw = kKeys * kRowBytes / 1024 / kPfWaves;  // copy instructions per wave per tile
+    static constexpr int kDc = HD / 32;  // 32-dim slices of a score product
+    static constexpr int kDt = HD / 16;  // 16-dim output blocks
+    static_assert(kKeys * kRowBytes == kTileBytes, "one tile = 16 KiB");
+};
+
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -85,7 +106,7 @@ struct PrefillArgs {
     const int64_t* starts;
     const int64_t* tables;
     const int64_t* lens;
-    void* ws_o;    // [max_chunks, T*Hq, D] partial outputs normalised by their sum (PartialOf<T>)
+    void* ws_o;    // [max_chunks, T*Hq, part_dim] partial outputs normalised by their sum (PartialOf<T>)
     float* ws_ml;  // [max_chunks, T*Hq, 2] (running max in log2 units, sum)
     int64_t ws_rows;  // T*Hq: one plane of partials per chunk index
     int64_t total_tokens;  // T: packed query rows (every row a sequence covers lies below it)
@@ -95,11 +116,12 @@ struct PrefillArgs {
     int q_heads;
     int kv_heads;
     int group;
-    int qb;        // query tokens per item (kPfRows / group, rounded down)
-    int chunk;     // keys per item (multiple of kPfKeys)
+    int qb;        // query tokens per item (rows of the tile shape / group, rounded down)
+    int chunk;     // keys per item (multiple of the tile's keys)
     int max_chunks;
     int chunk_choice;  // 1: a walk with more than one round of items may take a larger chunk
     int head_dim;
+    int part_dim;  // elements per partial row: the tile shape's padded head dim
     int64_t num_blocks;
     int block_size;
     int block_shift;  // log2(block_size) when a power of two, else -1
@@ -405,15 +427,18 @@ __device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, in
 }
 
 
-// One work item, computed by the whole work-group.  NARROW: head_dim is a
-// multiple of 8 below kPfD; rows are zero-padded to kPfD in LDS (the copies
+// One work item, computed by the whole work-group, in tiles of
+// PfShape<HD>.  NARROW: head_dim is a multiple of 8 below 128; rows are
+// zero-padded to 128 in LDS (the copies
 // skip the padded 16-byte chunks, which stay zero), the queries' padded dims
 // are zero, and only head_dim output dims are stored.
-template <typename T, int PAGES, bool NARROW>
+template <typename T, int PAGES, bool NARROW, int HD>
 __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a, const PrefillItem& item,
                                                             PrefillLds& lds) {
+    using SH = PfShape<HD>;
+    static_assert(!NARROW || HD == 128, "narrow heads pad to 128");
     constexpr bool SCALAR_PAGES = PAGES != kPagesPerLane;
-    const int hd = NARROW ? a.head_dim : kPfD;  // elements per K/V/Q/output row in memory
+    const int hd = NARROW ? a.head_dim : SH::kD;  // elements per K/V/Q/output row in memory
     const int dchunks = hd / 8;                 // 16-byte chunks per row
     auto& sm_k = lds.k;
     auto& sm_v = lds.v;
@@ -446,20 +471,20 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     const int chunk_len = __builtin_amdgcn_readfirstlane(item.chunk_len);
     const int chunk_start = chunk * chunk_len;
     const int chunk_end = min(chunk_start + chunk_len, kv_end);
-    const int t_begin = chunk_start / kPfKeys;
-    const int t_end = chunk_end > chunk_start ? (chunk_end + kPfKeys - 1) / kPfKeys : t_begin;
+    const int t_begin = chunk_start / SH::kKeys;
+    const int t_end = chunk_end > chunk_start ? (chunk_end + SH::kKeys - 1) / SH::kKeys : t_begin;
 
-    // The kPfNb 16-row column blocks of this wave.  Row r is token r % qb of
+    // The SH::kNb 16-row column blocks of this wave.  Row r is token r % qb of
     // the block and head r / qb of the group; when the group does not divide
-    // kPfRows the rows from qb * group on are idle (placed past the block's
+    // the tile's rows, those from qb * group on are idle (placed past the block's
     // tokens, so nothing reads or writes for them).
-    int qi[kPfNb], head[kPfNb], pos[kPfNb];
-    bool row_ok[kPfNb];
+    int qi[SH::kNb], head[SH::kNb], pos[SH::kNb];
+    bool row_ok[SH::kNb];
     int wave_last = -1, wave_first = 0x7fffffff;
     const int rows_used = a.qb * a.group;
 #pragma unroll
-    for (int nb = 0; nb < kPfNb; ++nb) {
-        const int r = wave * (16 * kPfNb) + nb * 16 + li;
+    for (int nb = 0; nb < SH::kNb; ++nb) {
+        const int r = wave * (16 * SH::kNb) + nb * 16 + li;
         const bool in_block = r < rows_used;
         qi[nb] = in_block ? q0 + r % a.qb : qlen;
         head[nb] = kvh * a.group + (in_block ? r / a.qb : 0);
@@ -491,15 +516,15 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     // m_run: the row's reference (log2 units, -inf until the row sees a key);
     // nref = -m_run, or 0 while there is no reference (masked keys then give
     // 2^-inf = 0 rather than NaN).
-    float m_run[kPfNb], nref[kPfNb], l_part[kPfNb];
-    f32x4 o[kPfNb][8];
+    float m_run[SH::kNb], nref[SH::kNb], l_part[SH::kNb];
+    f32x4 o[SH::kNb][SH::kDt];
 #pragma unroll
-    for (int nb = 0; nb < kPfNb; ++nb) {
+    for (int nb = 0; nb < SH::kNb; ++nb) {
         m_run[nb] = kNegInf;
         nref[nb] = 0.f;
         l_part[nb] = 0.f;
 #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) o[nb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int dt = 0; dt < SH::kDt; ++dt) o[nb][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
     // Swizzled LDS offsets this lane reads (independent of the tile):
@@ -508,17 +533,17 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     // store global chunk c in slot c ^ (row & 15); V rows in slot
     // c ^ (2*row & 15), so that the 16 lanes of a transposing read (4 rows x
     // 2 adjacent chunks) hit 8 different 16-byte bank groups.
-    int koff[4];
+    int koff[SH::kDc];
 #pragma unroll
-    for (int dc = 0; dc < 4; ++dc) koff[dc] = li * kRowBytes + 16 * ((4 * dc + lg) ^ li);
+    for (int dc = 0; dc < SH::kDc; ++dc) koff[dc] = li * SH::kRowBytes + 16 * ((4 * dc + lg) ^ li);
     const int vrow = 4 * lg + (li >> 2);
-    int voff[8];
+    int voff[SH::kDt];
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-        voff[dt] = vrow * kRowBytes + 16 * ((2 * dt + ((li & 3) >> 1)) ^ ((2 * vrow) & 15)) + 8 * (li & 1);
+    for (int dt = 0; dt < SH::kDt; ++dt)
+        voff[dt] = vrow * SH::kRowBytes + 16 * ((2 * dt + ((li & 3) >> 1)) ^ ((2 * vrow) & 15)) + 8 * (li & 1);
 
     // Copy plan: a tile's K (and V) is 16 instructions of 1 KiB; wave w issues
-    // instructions j = kPfIpw*w + i, each covering key rows 4j..4j+3 (lane ->
+    // instructions j = SH::kIpw*w + i, each covering key rows 4j..4j+3 (lane ->
     // row 4j + lane/16, LDS slot lane%16 = global chunk (lane%16)^(row&15) for
     // K, (lane%16)^(2*row&15) for V).
     const int64_t row_bytes_g = (int64_t)a.kv_heads * hd * 2;
@@ -526,13 +551,14 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     const uint8_t* kcache = static_cast<const uint8_t*>(a.key_cache) + (int64_t)kvh * hd * 2;
     const uint8_t* vcache = static_cast<const uint8_t*>(a.value_cache) + (int64_t)kvh * hd * 2;
     const int bs_shift = a.block_shift;
-    const int lrow = lane >> 4;  // row inside the instruction's 4 rows
-    uint32_t tile_off[kPfIpw], tile_off_v[kPfIpw];  // per-lane byte offsets of whole-tile copies from row 0
-    bool kchunk_ok[kPfIpw], vchunk_ok[kPfIpw];      // the lane's global chunk lies inside the row
+    const int lrow = lane / SH::kChunks;  // row inside the instruction's rows
+    const int lslot = lane % SH::kChunks;  // LDS slot of the lane's 16 bytes in that row
+    uint32_t tile_off[SH::kIpw], tile_off_v[SH::kIpw];  // per-lane byte offsets of whole-tile copies from row 0
+    bool kchunk_ok[SH::kIpw], vchunk_ok[SH::kIpw];      // the lane's global chunk lies inside the row
 #pragma unroll
-    for (int i = 0; i < kPfIpw; ++i) {
-        const int row = 4 * (kPfIpw * wave + i) + lrow;
-        const int kc = (lane & 15) ^ (row & 15), vc = (lane & 15) ^ ((2 * row) & 15);
+    for (int i = 0; i < SH::kIpw; ++i) {
+        const int row = SH::kRowsPerInst * (SH::kIpw * wave + i) + lrow;
+        const int kc = lslot ^ (row & 15), vc = lslot ^ ((2 * row) & 15);
         kchunk_ok[i] = !NARROW || kc < dchunks;
         vchunk_ok[i] = !NARROW || vc < dchunks;
         tile_off[i] = (uint32_t)(row * row_bytes_g) + 16u * (uint32_t)(kchunk_ok[i] ? kc : 0);
@@ -561,7 +587,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     int tile_base = t_begin;
     int64_t tile_pages = -1, next_pages = -1;
     auto window_pages = [&](int base) -> int64_t {
-        const int key0 = (base + lane) * kPfKeys;
+        const int key0 = (base + lane) * SH::kKeys;
         int64_t raw = -1;
         if (key0 < chunk_end) raw = table[key0 >> bs_shift];
         return raw;
@@ -574,24 +600,24 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     // Bit st: the tile in ring stage st lies in one present page with all of
     // its 64 keys in the chunk (set by every wave when it issues the copies).
     uint32_t full_stages = 0;
-    int pg_next[kPfIpw];  // pages for the next tile to issue
+    int pg_next[SH::kIpw];  // pages for the next tile to issue
     auto lookup = [&](int tile) {
         if constexpr (PAGES == kPagesPerTile) {
             const int pg = page_of_tile(tile);
 #pragma unroll
-            for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pg;
+            for (int i = 0; i < SH::kIpw; ++i) pg_next[i] = pg;
         } else {
 #pragma unroll
-            for (int i = 0; i < kPfIpw; ++i) {
-                const int row = 4 * (kPfIpw * wave + i) + (SCALAR_PAGES ? 0 : lrow);
-                pg_next[i] = page_at(tile * kPfKeys + row);
+            for (int i = 0; i < SH::kIpw; ++i) {
+                const int row = SH::kRowsPerInst * (SH::kIpw * wave + i) + (SCALAR_PAGES ? 0 : lrow);
+                pg_next[i] = page_at(tile * SH::kKeys + row);
             }
         }
     };
     auto issue = [&](int tile, int st) {
         if constexpr (PAGES == kPagesPerTile) {
-            const int key0 = tile * kPfKeys;
-            const bool full = pg_next[0] >= 0 && key0 + kPfKeys - 1 < chunk_end;
+            const int key0 = tile * SH::kKeys;
+            const bool full = pg_next[0] >= 0 && key0 + SH::kKeys - 1 < chunk_end;
             full_stages = full ? (full_stages | (1u << st)) : (full_stages & ~(1u << st));
             if (full) {
                 // Full tile in one page: one scalar base for all copies.
@@ -599,8 +625,8 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     (int64_t)pg_next[0] * page_bytes_g + (int64_t)(key0 & (a.block_size - 1)) * row_bytes_g;
                 const uint32_t lk = lds_addr(&sm_k[st][0]), lv = lds_addr(&sm_v[st][0]);
 #pragma unroll
-                for (int i = 0; i < kPfIpw; ++i) {
-                    const int j = kPfIpw * wave + i;
+                for (int i = 0; i < SH::kIpw; ++i) {
+                    const int j = SH::kIpw * wave + i;
                     if (kchunk_ok[i]) lds_dma16_s(kcache + base, tile_off[i], lk + 1024 * j);
                     if (vchunk_ok[i]) lds_dma16_s(vcache + base, tile_off_v[i], lv + 1024 * j);
                 }
@@ -609,12 +635,12 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         }
         bool all_ok = true;
 #pragma unroll
-        for (int i = 0; i < kPfIpw; ++i) {
-            const int j = kPfIpw * wave + i;
-            const int row = 4 * j + lrow;
-            const int key = tile * kPfKeys + row;
-            const int cidx = (lane & 15) ^ (row & 15);
-            const int cidx_v = (lane & 15) ^ ((2 * row) & 15);
+        for (int i = 0; i < SH::kIpw; ++i) {
+            const int j = SH::kIpw * wave + i;
+            const int row = SH::kRowsPerInst * j + lrow;
+            const int key = tile * SH::kKeys + row;
+            const int cidx = lslot ^ (row & 15);
+            const int cidx_v = lslot ^ ((2 * row) & 15);
             const int page = pg_next[i];
             // Rows past the chunk inside a valid first-row page are masked too.
             const bool ok = page >= 0 && key < chunk_end;
@@ -630,7 +656,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             }
             lds_dma16(gk, lds_addr(&sm_k[st][0]) + 1024 * j);
             lds_dma16(gv, lds_addr(&sm_v[st][0]) + 1024 * j);
-            if ((lane & 15) == 0) sm_b[st][row] = ok ? 0.f : kNegInf;
+            if (lslot == 0) sm_b[st][row] = ok ? 0.f : kNegInf;
         }
         const bool wave_full = __builtin_amdgcn_ballot_w64(!all_ok) == 0;
         if (lane == 0) sm_full[st][wave] = wave_full ? 1 : 0;
@@ -639,12 +665,12 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     // Q^T operands: row (nb, li), d = 32*dc + 8*lg .. +8.  Their latency
     // overlaps the first pair's copies: the first pair barrier waits for the
     // whole vector-memory counter.
-    u32x4 qop[kPfNb][4];
+    u32x4 qop[SH::kNb][SH::kDc];
 #pragma unroll
-    for (int nb = 0; nb < kPfNb; ++nb) {
+    for (int nb = 0; nb < SH::kNb; ++nb) {
         const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + ((row0 + qi[nb]) * a.q_heads + head[nb]) * hd;
 #pragma unroll
-        for (int dc = 0; dc < 4; ++dc) {
+        for (int dc = 0; dc < SH::kDc; ++dc) {
             qop[nb][dc] = u32x4{0u, 0u, 0u, 0u};
             if (row_ok[nb] && (!NARROW || 32 * dc + 8 * lg < hd))
                 qop[nb][dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
@@ -659,11 +685,11 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             // A scalar lookup: the window's vector load is first needed after
             // the first barrier, so nothing waits for it (or for the queries)
             // before these copies go out.
-            const int key0 = t_begin * kPfKeys;
+            const int key0 = t_begin * SH::kKeys;
             const int64_t page = ctable[key0 >> bs_shift];
             const int pg = (key0 < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
 #pragma unroll
-            for (int i = 0; i < kPfIpw; ++i) pg_next[i] = pg;
+            for (int i = 0; i < SH::kIpw; ++i) pg_next[i] = pg;
         } else {
             lookup(t_begin);
         }
@@ -706,7 +732,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             const int tile = tp + k;
             if (tile < t_begin) continue;  // the prologue's virtual first slot
             const int st = (st0 + k) & (kPfStages - 1);
-            const int tile0 = tile * kPfKeys;
+            const int tile0 = tile * SH::kKeys;
             if (tile0 <= wave_last) {
                 const uint8_t* smk = &sm_k[st][0];
                 const float* smb = &sm_b[st][0];
@@ -721,19 +747,19 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     const int4 fb = *reinterpret_cast<const int4*>(&sm_full[st][4]);
                     full = (fa.x & fa.y & fa.z & fa.w & fb.x & fb.y & fb.z & fb.w) != 0;
                 }
-                const bool fast = full && tile0 + kPfKeys - 1 <= wave_first;
+                const bool fast = full && tile0 + SH::kKeys - 1 <= wave_first;
                 typedef __attribute__((address_space(3))) uint8_t lds_u8;
                 lds_u8* vbase = (lds_u8*)&sm_v[st][0];
                 // Two halves of 32 keys: S^T -> probabilities each, then
                 // O^T += V^T P^T over the whole tile, two products back to back
                 // per accumulator.
-                u32x4 pops[2][kPfNb];
+                u32x4 pops[SH::kHalves][SH::kNb];
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
+                for (int h = 0; h < SH::kHalves; ++h) {
                     // S^T = K Q^T for key sub-tiles 2h, 2h+1: 8 independent accumulators.
-                    f32x4 sc[kPfNb][2];
+                    f32x4 sc[SH::kNb][2];
 #pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) sc[nb][0] = sc[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int nb = 0; nb < SH::kNb; ++nb) sc[nb][0] = sc[nb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
                     // Each accumulator takes its four products back to back: the
                     // matrix core forwards a result straight into the next
                     // product of the same accumulator, while alternating between
@@ -742,18 +768,18 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     // issues MFMAs, the other wave of its SIMD runs softmax VALU
                     // work in the gaps rather than competing for the same slots.
                     __builtin_amdgcn_s_setprio(1);
-                    u32x4 kop[2][4];
+                    u32x4 kop[2][SH::kDc];
 #pragma unroll
-                    for (int dc = 0; dc < 4; ++dc) {
-                        kop[0][dc] = *reinterpret_cast<const u32x4*>(smk + 32 * h * kRowBytes + koff[dc]);
-                        kop[1][dc] = *reinterpret_cast<const u32x4*>(smk + (32 * h + 16) * kRowBytes + koff[dc]);
+                    for (int dc = 0; dc < SH::kDc; ++dc) {
+                        kop[0][dc] = *reinterpret_cast<const u32x4*>(smk + 32 * h * SH::kRowBytes + koff[dc]);
+                        kop[1][dc] = *reinterpret_cast<const u32x4*>(smk + (32 * h + 16) * SH::kRowBytes + koff[dc]);
                     }
 #pragma unroll
                     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-                        for (int nb = 0; nb < kPfNb; ++nb) {
+                        for (int nb = 0; nb < SH::kNb; ++nb) {
 #pragma unroll
-                            for (int dc = 0; dc < 4; ++dc)
+                            for (int dc = 0; dc < SH::kDc; ++dc)
                                 sc[nb][kk] = T::mfma16x16x32(kop[kk][dc], qop[nb][dc], sc[nb][kk]);
                             __builtin_amdgcn_sched_barrier(0);  // keep the chain contiguous
                         }
@@ -763,7 +789,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     __builtin_amdgcn_s_setprio(0);
                     if (!fast) {
 #pragma unroll
-                        for (int nb = 0; nb < kPfNb; ++nb) {
+                        for (int nb = 0; nb < SH::kNb; ++nb) {
                             const int lim = pos[nb] - tile0 - 32 * h - 4 * lg;  // key (16*kk + j) must be <= lim
 #pragma unroll
                             for (int kk = 0; kk < 2; ++kk) {
@@ -782,10 +808,10 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     // No row maximum on the common path: the reference only has to
                     // keep every probability small, which the sum of a lane's
                     // probabilities checks after the fact (inf and NaN included).
-                    float p[kPfNb][8], dl[kPfNb];
+                    float p[SH::kNb][8], dl[SH::kNb];
                     bool need = false;
 #pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) {
+                    for (int nb = 0; nb < SH::kNb; ++nb) {
 #pragma unroll
                         for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
@@ -801,7 +827,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                         // Exact step: row maxima over the 4 lanes of each row,
                         // rescale what is accumulated, recompute the probabilities.
 #pragma unroll
-                        for (int nb = 0; nb < kPfNb; ++nb) {
+                        for (int nb = 0; nb < SH::kNb; ++nb) {
                             float r = kNegInf;
 #pragma unroll
                             for (int kk = 0; kk < 2; ++kk)
@@ -812,7 +838,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                             m_run[nb] = mn;
                             l_part[nb] *= alpha;
 #pragma unroll
-                            for (int dt = 0; dt < 8; ++dt) o[nb][dt] *= alpha;
+                            for (int dt = 0; dt < SH::kDt; ++dt) o[nb][dt] *= alpha;
                             if (h == 1) {
                                 // The first half's products are still to be accumulated.
 #pragma unroll
@@ -833,7 +859,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     // Packed as the B operand of the PV products:
                     // k-slot 4*kk + j <-> key 32h + 16kk + 4*lg + j.
 #pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) {
+                    for (int nb = 0; nb < SH::kNb; ++nb) {
                         l_part[nb] += dl[nb];
                         pops[h][nb] = u32x4{T::pack(p[nb][0], p[nb][1]), T::pack(p[nb][2], p[nb][3]),
                                             T::pack(p[nb][4], p[nb][5]), T::pack(p[nb][6], p[nb][7])};
@@ -841,32 +867,33 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 }
                 // O^T += V^T P^T over the tile; V^T operands by transposing reads,
                 // one dim block ahead of the products that use them.
-                auto vread = [&](int dt, u32x4 (&vop)[2]) __attribute__((always_inline)) {
+                auto vread = [&](int dt, u32x4 (&vop)[SH::kHalves]) __attribute__((always_inline)) {
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
+                    for (int h = 0; h < SH::kHalves; ++h) {
                         const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (lds_s16x4*)(vbase + 32 * h * kRowBytes + voff[dt]));
+                            (lds_s16x4*)(vbase + 32 * h * SH::kRowBytes + voff[dt]));
                         const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (lds_s16x4*)(vbase + (32 * h + 16) * kRowBytes + voff[dt]));
+                            (lds_s16x4*)(vbase + (32 * h + 16) * SH::kRowBytes + voff[dt]));
                         const u32x2 w0 = __builtin_bit_cast(u32x2, t0);
                         const u32x2 w1 = __builtin_bit_cast(u32x2, t1);
                         vop[h] = u32x4{w0[0], w0[1], w1[0], w1[1]};
                     }
                 };
                 __builtin_amdgcn_s_setprio(1);
-                u32x4 vcur[2], vnext[2];
+                u32x4 vcur[SH::kHalves], vnext[SH::kHalves];
                 vread(0, vcur);
 #pragma unroll
-                for (int dt = 0; dt < 8; ++dt) {
-                    if (dt + 1 < 8) vread(dt + 1, vnext);
+                for (int dt = 0; dt < SH::kDt; ++dt) {
+                    if (dt + 1 < SH::kDt) vread(dt + 1, vnext);
 #pragma unroll
-                    for (int nb = 0; nb < kPfNb; ++nb) {
-                        o[nb][dt] = T::mfma16x16x32(vcur[0], pops[0][nb], o[nb][dt]);
-                        o[nb][dt] = T::mfma16x16x32(vcur[1], pops[1][nb], o[nb][dt]);
-                        __builtin_amdgcn_sched_barrier(0);  // keep the two products back to back
+                    for (int nb = 0; nb < SH::kNb; ++nb) {
+#pragma unroll
+                        for (int h = 0; h < SH::kHalves; ++h)
+                            o[nb][dt] = T::mfma16x16x32(vcur[h], pops[h][nb], o[nb][dt]);
+                        __builtin_amdgcn_sched_barrier(0);  // keep the products back to back
                     }
-                    vcur[0] = vnext[0];
-                    vcur[1] = vnext[1];
+#pragma unroll
+                    for (int h = 0; h < SH::kHalves; ++h) vcur[h] = vnext[h];
                 }
                 __builtin_amdgcn_s_setprio(0);
             }
@@ -876,7 +903,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     wait_vmcnt_all();
 
 #pragma unroll
-    for (int nb = 0; nb < kPfNb; ++nb) {
+    for (int nb = 0; nb < SH::kNb; ++nb) {
         const float l_row = row4_sum(l_part[nb]);
         if (qi[nb] >= qlen) continue;
         const int64_t rowid = (row0 + qi[nb]) * a.q_heads + head[nb];
@@ -884,7 +911,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             const float inv = (row_ok[nb] && l_row > 0.f) ? __builtin_amdgcn_rcpf(l_row) : 0.f;
             uint16_t* orow = static_cast<uint16_t*>(a.out) + rowid * hd;
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
+            for (int dt = 0; dt < SH::kDt; ++dt) {
                 const u32x2 w = {T::pack(o[nb][dt][0] * inv, o[nb][dt][1] * inv),
                                  T::pack(o[nb][dt][2] * inv, o[nb][dt][3] * inv)};
                 if (!NARROW || 16 * dt + 4 * lg < hd) *reinterpret_cast<u32x2*>(orow + 16 * dt + 4 * lg) = w;
@@ -893,9 +920,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             const int64_t slot = (int64_t)chunk * a.ws_rows + rowid;
             const float inv = (row_ok[nb] && l_row > 0.f) ? __builtin_amdgcn_rcpf(l_row) : 0.f;
             using P = typename PartialOf<T>::type;
-            P* po = static_cast<P*>(a.ws_o) + slot * kPfD;
+            P* po = static_cast<P*>(a.ws_o) + slot * SH::kD;
 #pragma unroll
-            for (int dt = 0; dt < 8; ++dt) {
+            for (int dt = 0; dt < SH::kDt; ++dt) {
                 if constexpr (sizeof(P) == 4) {
                     *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * lg) = o[nb][dt] * inv;
                 } else {
@@ -932,18 +959,20 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 // which), so the count costs a quarter of the blocks per thread; the sums
 // meet in the K ring, which the first copies fill only after the final
 // barrier here.
-constexpr float kItemFixedTiles = 2.5f;
+constexpr float kItemFixedTiles = 2.5f;  // in 64-key tiles
 constexpr int kChoiceCands = 128;
 constexpr int kChoiceSlices = kPfThreads / kChoiceCands;
 
+template <int KEYS>
 __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta& first) {
+    constexpr float kFixed = kItemFixedTiles * 64.f / KEYS;  // an item's fixed cost in tiles of KEYS keys
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
     const int ci = tid % kChoiceCands, slice = tid / kChoiceCands;
     const int cap = a.table_width * a.block_size;
-    const int cmax = (cap + kPfKeys - 1) / kPfKeys * kPfKeys;
-    const int span = (cmax - a.chunk) / kPfKeys;  // candidate steps above the minimum
+    const int cmax = (cap + KEYS - 1) / KEYS * KEYS;
+    const int span = (cmax - a.chunk) / KEYS;  // candidate steps above the minimum
     const int step = max(1, (span + kChoiceCands - 1) / kChoiceCands);
-    const int cand = a.chunk + kPfKeys * step * ci;
+    const int cand = a.chunk + KEYS * step * ci;
     const bool valid = cand <= cmax;  // candidate 0, the minimum, always is
     uint32_t items = 0, tiles = 0;
     if (__builtin_amdgcn_ballot_w64(valid) != 0) {  // wave-uniform
@@ -960,7 +989,7 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
                      k += kChoiceSlices) {
                     const uint32_t e = (uint32_t)block_kv_end(a, sj, cj, nj, (int64_t)k * a.qb);
                     items += e > 0 ? ceil_div_u32(e, (uint32_t)cand) : 1;
-                    tiles += (e + kPfKeys - 1) / kPfKeys;
+                    tiles += (e + KEYS - 1) / KEYS;
                 }
                 blk += nb;
             }
@@ -981,8 +1010,8 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
         }
         const uint32_t w = (uint32_t)a.item_stride;
         const float rounds = (float)((it_sum + w - 1) / w);
-        const float cost = fmaxf(rounds * (kItemFixedTiles + (float)(cand / kPfKeys)),
-                                 ((float)tl_sum + kItemFixedTiles * (float)it_sum) / (float)w);
+        const float cost = fmaxf(rounds * (kFixed + (float)(cand / KEYS)),
+                                 ((float)tl_sum + kFixed * (float)it_sum) / (float)w);
         // Non-negative floats order like their bit patterns.
         key = ((uint64_t)__float_as_uint(cost) << 32) | (uint32_t)ci;
     }
@@ -998,7 +1027,7 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
 #pragma unroll
     for (int w = 1; w < kPfWaves; ++w) best = lds.pick[w] < best ? lds.pick[w] : best;
     __syncthreads();  // every thread has read the sums and picks before the ring is refilled
-    return a.chunk + kPfKeys * step * (int)(uint32_t)best;
+    return a.chunk + KEYS * step * (int)(uint32_t)best;
 }
 
 // Items are enumerated densely.  WALK = false: one item per work-group (the
@@ -1006,7 +1035,7 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
 // true: one work-group per CU slot, each walking items idx, idx +
 // item_stride, ... below the item count (a separate instantiation, so that
 // the one-item kernel keeps its register allocation).
-template <typename T, int PAGES, bool WALK, bool NARROW>
+template <typename T, int PAGES, bool WALK, bool NARROW, int HD>
 __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) PrefillLds lds;
     if constexpr (NARROW && PAGES == kPagesPerTile) {
@@ -1021,7 +1050,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
     if constexpr (!WALK) {
         PrefillItem item;
         if (!find_item(a, a.chunk, blockIdx.x / a.kv_heads, item)) return;
-        prefill_item<T, PAGES, NARROW>(a, item, lds);
+        prefill_item<T, PAGES, NARROW, HD>(a, item, lds);
     } else {
         // The first lookup also counts the items, so that the walk ends
         // without a lookup past the end.
@@ -1040,7 +1069,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
             total = walk_index(a, chunk_len, m, lds, cnt, incl);
             if (a.chunk_choice && total > a.item_stride) {
                 // More than one round of items: the lengths decide the chunk.
-                chunk_len = choose_chunk(a, lds, m);
+                chunk_len = choose_chunk<PfShape<HD>::kKeys>(a, lds, m);
                 total = walk_index(a, chunk_len, m, lds, cnt, incl);
             }
             // The first lookup uses this wave's own copy of the index; wave 0's
@@ -1050,12 +1079,12 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
             ok = find_item(a, chunk_len, idx, item, &total);
             if (a.chunk_choice && total > a.item_stride) {
                 const SeqMeta m = load_meta(a, (int)(threadIdx.x & (kWave - 1)));
-                chunk_len = choose_chunk(a, lds, m);
+                chunk_len = choose_chunk<PfShape<HD>::kKeys>(a, lds, m);
                 ok = find_item(a, chunk_len, idx, item, &total);
             }
         }
         while (ok) {
-            prefill_item<T, PAGES, NARROW>(a, item, lds);
+            prefill_item<T, PAGES, NARROW, HD>(a, item, lds);
             idx += a.item_stride;
             if (idx >= total) break;
             __syncthreads();  // every wave is done with the LDS ring before the next item refills it
@@ -1069,8 +1098,9 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
 // chunks: with o_c the chunk's normalised output, l_c its probability sum and
 // m_c its reference, out = sum_c w_c o_c / sum_c w_c, w_c = l_c 2^(m_c - M).
 // One work-group per packed token (its chunk count comes from the attention
-// kernel); a thread handles 8 dims of one head.  Partial rows are kPfD wide
-// (heads narrower than kPfD are zero-padded there); the output has head_dim.
+// kernel); a thread handles 8 dims of one head.  Partial rows are part_dim
+// wide (heads narrower than 128 are zero-padded there); the output has
+// head_dim.
 constexpr int kMergeThreads = 256;
 
 template <typename T>
@@ -1104,7 +1134,7 @@ __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(Pref
             for (int k = 0; k < kGroup; ++k) {
                 const int c = min(c0 + k, nchunks - 1);
                 const int64_t slot = (int64_t)c * a.ws_rows + rowid;
-                const u32x4* po = reinterpret_cast<const u32x4*>(static_cast<const P*>(a.ws_o) + slot * kPfD + d0);
+                const u32x4* po = reinterpret_cast<const u32x4*>(static_cast<const P*>(a.ws_o) + slot * a.part_dim + d0);
                 raw[k][0] = po[0];
                 if constexpr (sizeof(P) == 4) raw[k][1] = po[1];
                 mlc[k] = ml[(int64_t)c * a.ws_rows];
@@ -1278,7 +1308,9 @@ int check_prefill(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64
 
 struct PrefillPlan {
     bool mfma;
-    bool narrow;  // head_dim below kPfD, zero-padded in LDS
+    bool narrow;  // head_dim below 128, zero-padded in LDS
+    int hd;       // tile shape: padded head dim (128 or 256)
+    int keys;     // keys per tile of that shape
     int qb;
     int chunk;
     int max_chunks;
@@ -1297,25 +1329,31 @@ PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_
                               int64_t head_dim, int64_t block_size, int64_t table_width, int64_t chunk_tokens) {
     PrefillPlan p{};
     const int64_t group = q_heads / kv_heads;
-    // MFMA tiles for head_dim 128, and for narrower multiples of 8 padded to
-    // 128 in LDS (zero dims add nothing to the scores and give zero outputs).
-    p.narrow = head_dim < kPfD;
-    p.mfma = group <= kPfRows && (head_dim == kPfD || (head_dim % 8 == 0 && head_dim >= 8 && p.narrow));
+    // MFMA tiles for head_dim 128 and 256, and for narrower multiples of 8
+    // padded to 128 in LDS (zero dims add nothing to the scores and give zero
+    // outputs).
+    const bool wide = head_dim == 256;
+    p.narrow = head_dim < 128;
+    p.hd = wide ? 256 : 128;
+    p.keys = wide ? PfShape<256>::kKeys : PfShape<128>::kKeys;
+    const int rows = wide ? PfShape<256>::kRows : PfShape<128>::kRows;
+    p.mfma = group <= rows && (head_dim == 128 || wide || (head_dim % 8 == 0 && head_dim >= 8 && p.narrow));
     if (!p.mfma) return p;
-    p.qb = (int)(kPfRows / group);
+    p.qb = (int)(rows / group);
+    const int64_t keys = p.keys;
     const int64_t cap = table_width * block_size;
-    const int64_t cap_tiles = (cap + kPfKeys - 1) / kPfKeys * kPfKeys;
+    const int64_t cap_tiles = (cap + keys - 1) / keys * keys;
     const int64_t blocks_bound = (total_tokens + p.qb - 1) / p.qb + num_seqs;
     int64_t chunk;
-    if (chunk_tokens > 0) chunk = (chunk_tokens + kPfKeys - 1) / kPfKeys * kPfKeys;
+    if (chunk_tokens > 0) chunk = (chunk_tokens + keys - 1) / keys * keys;
     // The split test counts the query blocks the tokens fill at least (the
     // bound above adds one partial block per sequence): near the threshold,
     // ragged contexts make whole-context items uneven, and the walk's chunk
     // choice can still take chunks as long as the capacity.
     else if ((total_tokens + p.qb - 1) / p.qb * kv_heads >= kPrefillCUs + kPrefillCUs / 2) chunk = cap_tiles;
-    else chunk = std::max<int64_t>(512, ((cap + 31) / 32 + kPfKeys - 1) / kPfKeys * kPfKeys);
+    else chunk = std::max<int64_t>(512, ((cap + 31) / 32 + keys - 1) / keys * keys);
     if (chunk > cap_tiles) chunk = cap_tiles;
-    if (chunk < kPfKeys) chunk = kPfKeys;
+    if (chunk < keys) chunk = keys;
     p.chunk = (int)chunk;
     p.max_chunks = (int)((cap + chunk - 1) / chunk);
     if (p.max_chunks < 1) p.max_chunks = 1;
@@ -1330,11 +1368,12 @@ PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_
 struct PrefillWorkspace {
     size_t ml_offset, tok_offset, bytes;
 };
-PrefillWorkspace prefill_workspace_layout(int64_t rows, int64_t max_chunks, int64_t tokens, int dtype) {
+PrefillWorkspace prefill_workspace_layout(int64_t rows, int64_t max_chunks, int64_t tokens, int dtype,
+                                          int64_t part_dim) {
     const size_t part_elem = dtype == MVME_BF16 ? sizeof(uint16_t) : sizeof(float);
     auto align16 = [](size_t n) { return (n + 15) / 16 * 16; };
     PrefillWorkspace w{};
-    w.ml_offset = align16((size_t)max_chunks * rows * kPfD * part_elem);
+    w.ml_offset = align16((size_t)max_chunks * rows * part_dim * part_elem);
     w.tok_offset = w.ml_offset + align16((size_t)max_chunks * rows * 2 * sizeof(float));
     w.bytes = w.tok_offset + align16((size_t)tokens * sizeof(int));
     return w;
@@ -1359,7 +1398,7 @@ extern "C" size_t mvme_paged_prefill_workspace_size(int64_t num_seqs, int64_t to
     const PrefillPlan p = make_prefill_plan(num_seqs, total_tokens, q_heads, kv_heads, head_dim, block_size,
                                             table_width, chunk_tokens);
     if (!p.mfma || p.max_chunks <= 1) return 0;
-    return prefill_workspace_layout(total_tokens * q_heads, p.max_chunks, total_tokens, dtype).bytes;
+    return prefill_workspace_layout(total_tokens * q_heads, p.max_chunks, total_tokens, dtype, p.hd).bytes;
 }
 
 extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void* key_cache,
@@ -1409,6 +1448,7 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         if (table_width * block_size > 2147483647)
             return fail(MVME_EINVAL, "paged prefill table capacity exceeds 2^31 tokens");
         a.qb = p.qb;
+        a.part_dim = p.hd;
         a.chunk = p.chunk;
         a.max_chunks = p.max_chunks;
         a.ws_rows = total_tokens * q_heads;
@@ -1416,7 +1456,7 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         a.chunk_choice = chunk_tokens <= 0 ? 1 : 0;
         if (need > 0) {
             const PrefillWorkspace w = prefill_workspace_layout(total_tokens * q_heads, p.max_chunks, total_tokens,
-                                                                dtype);
+                                                                dtype, p.hd);
             a.ws_o = workspace;
             a.ws_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + w.ml_offset);
             a.ws_tok = reinterpret_cast<int*>(static_cast<uint8_t*>(workspace) + w.tok_offset);
@@ -1437,8 +1477,10 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         }
         const int64_t groups = item_slots * kv_heads;
         if (groups > 2147483647) return fail(MVME_EINVAL, "paged prefill grid too large");
-        // Whole-tile pages need 32-bit per-lane offsets inside a tile.
-        const bool tile_pages = a.block_shift >= 6 && kv_heads * head_dim * 2 * kPfKeys < (int64_t(1) << 31);
+        // Whole-tile pages: a tile lies in one page (power-of-two blocks of at
+        // least a tile's keys) and per-lane offsets inside a tile fit 32 bits.
+        const bool tile_pages = a.block_shift >= 0 && block_size >= p.keys &&
+                                kv_heads * head_dim * 2 * p.keys < (int64_t(1) << 31);
         int pages = tile_pages ? kPagesPerTile : (block_size % 4 == 0 ? kPagesPerRows : kPagesPerLane);
         if (p.narrow && pages == kPagesPerRows) pages = kPagesPerLane;  // no narrow instantiation of that mode
         const dim3 grid((unsigned)groups), block(kPfThreads);
@@ -1449,22 +1491,32 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         };
         auto launch_type = [&](auto type_tag) {
             using T = decltype(type_tag);
-            if (p.narrow) {
+            if (p.hd == 256) {
                 if (pages == kPagesPerTile)
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true>,
-                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true>);
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 256>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 256>);
+                else if (pages == kPagesPerRows)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerRows, false, false, 256>,
+                                paged_prefill_mfma_kernel<T, kPagesPerRows, true, false, 256>);
                 else
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, true>,
-                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, true>);
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, false, 256>,
+                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, false, 256>);
+            } else if (p.narrow) {
+                if (pages == kPagesPerTile)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true, 128>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true, 128>);
+                else
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, true, 128>,
+                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, true, 128>);
             } else if (pages == kPagesPerTile) {
-                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false>,
-                            paged_prefill_mfma_kernel<T, kPagesPerTile, true, false>);
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 128>,
+                            paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 128>);
             } else if (pages == kPagesPerRows) {
-                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerRows, false, false>,
-                            paged_prefill_mfma_kernel<T, kPagesPerRows, true, false>);
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerRows, false, false, 128>,
+                            paged_prefill_mfma_kernel<T, kPagesPerRows, true, false, 128>);
             } else {
-                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, false>,
-                            paged_prefill_mfma_kernel<T, kPagesPerLane, true, false>);
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, false, 128>,
+                            paged_prefill_mfma_kernel<T, kPagesPerLane, true, false, 128>);
             }
         };
         if (dtype == MVME_FP16) launch_type(Half{});

@@ -277,11 +277,27 @@ def test_mfma_prefill_narrow_heads(head_dim, block, chunk_tokens, dtype, heads, 
     assert max_err(actual, c_oracle.paged_prefill(*args, block)) <= GATE[dtype]
 
 
-@pytest.mark.parametrize("head_dim,block,dtype", [(100, 16, torch.bfloat16), (256, 256, torch.float16),
+@pytest.mark.parametrize("block,chunk_tokens,dtype,heads,kv_heads", [
+    (256, 0, torch.bfloat16, 16, 8), (256, 256, torch.float16, 16, 8), (32, 0, torch.bfloat16, 40, 8),
+    (16, 0, torch.bfloat16, 8, 1), (5, 320, torch.float16, 28, 4), (64, 96, torch.bfloat16, 100, 100),
+])
+def test_mfma_prefill_head_dim_256(block, chunk_tokens, dtype, heads, kv_heads):
+    """head_dim 256 runs the MFMA kernel with 16 query rows per wave and
+    32-key tiles: whole-tile copies (blocks 256, 64, 32), per-row-pair copies
+    (block 16), per-row copies (block 5), key splits with 256-wide partials,
+    and GQA groups 2, 5, 8, 7 and 1."""
+    args = _two_sequence_case(256, heads, kv_heads, block, dtype, seed=block + chunk_tokens)
+    print(f"prefill D=256 block={block} chunk={chunk_tokens} {dtype} {heads}/{kv_heads}", flush=True)
+    actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip", chunk_tokens=chunk_tokens)
+    assert max_err(actual, paged_oracle.paged_prefill_attention(*args, block, cast=False)) <= GATE[dtype]
+    assert max_err(actual, c_oracle.paged_prefill(*args, block)) <= GATE[dtype]
+
+
+@pytest.mark.parametrize("head_dim,block,dtype", [(100, 16, torch.bfloat16), (192, 256, torch.float16),
                                                   (12, 4, torch.float16)])
 def test_generic_prefill_other_head_dims(head_dim, block, dtype):
-    """Head dims the MFMA kernel does not take (above 128, or not a multiple
-    of 8) run the one-wave-per-row kernel."""
+    """Head dims the MFMA kernel does not take (not a multiple of 8, or above
+    128 other than 256) run the one-wave-per-row kernel."""
     args = _two_sequence_case(head_dim, 8, 4, block, dtype, seed=head_dim)
     print(f"generic prefill D={head_dim} block={block} {dtype}", flush=True)
     actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip")
