@@ -210,9 +210,10 @@ int mvme_paged_attention_decode_write(void* out, const void* query, void* key_ca
  * Bytes of device workspace mvme_paged_prefill_attention needs for these
  * shapes and element type (0 when no query block is split over key chunks).
  * Pure host function.  chunk_tokens: 0 selects the library's default key
- * chunking.  Layout: the key-chunk partial outputs (2-byte elements for
- * MVME_BF16, 4-byte for MVME_FP16), their fp32 (reference, sum) pairs, and
- * one int per packed token.
+ * chunking.  Layout: the key-chunk partial outputs (rows 128 wide for
+ * head_dim <= 128, 256 wide for 256; 2-byte elements for MVME_BF16, 4-byte
+ * for MVME_FP16), their fp32 (reference, sum) pairs, and one int per packed
+ * token.
  */
 size_t mvme_paged_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
                                          int64_t kv_heads, int64_t head_dim, int64_t block_size,
