@@ -428,15 +428,14 @@ __device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, in
 
 
 // One work item, computed by the whole work-group, in tiles of
-// PfShape<HD>.  NARROW: head_dim is a multiple of 8 below 128; rows are
-// zero-padded to 128 in LDS (the copies
-// skip the padded 16-byte chunks, which stay zero), the queries' padded dims
-// are zero, and only head_dim output dims are stored.
+// PfShape<HD>.  NARROW: head_dim is a multiple of 8 below HD; rows are
+// zero-padded to HD in LDS (the copies skip the padded 16-byte chunks,
+// which stay zero), the queries' padded dims are zero, and only head_dim
+// output dims are stored.
 template <typename T, int PAGES, bool NARROW, int HD>
 __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a, const PrefillItem& item,
                                                             PrefillLds& lds) {
     using SH = PfShape<HD>;
-    static_assert(!NARROW || HD == 128, "narrow heads pad to 128");
     constexpr bool SCALAR_PAGES = PAGES != kPagesPerLane;
     const int hd = NARROW ? a.head_dim : SH::kD;  // elements per K/V/Q/output row in memory
     const int dchunks = hd / 8;                 // 16-byte chunks per row
@@ -1099,7 +1098,7 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
 // m_c its reference, out = sum_c w_c o_c / sum_c w_c, w_c = l_c 2^(m_c - M).
 // One work-group per packed token (its chunk count comes from the attention
 // kernel); a thread handles 8 dims of one head.  Partial rows are part_dim
-// wide (heads narrower than 128 are zero-padded there); the output has
+// wide (heads narrower than the tile shape are zero-padded there); the output has
 // head_dim.
 constexpr int kMergeThreads = 256;
 
@@ -1308,7 +1307,7 @@ int check_prefill(int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64
 
 struct PrefillPlan {
     bool mfma;
-    bool narrow;  // head_dim below 128, zero-padded in LDS
+    bool narrow;  // head_dim below the tile shape's, zero-padded in LDS
     int hd;       // tile shape: padded head dim (128 or 256)
     int keys;     // keys per tile of that shape
     int qb;
@@ -1329,15 +1328,16 @@ PrefillPlan make_prefill_plan(int64_t num_seqs, int64_t total_tokens, int64_t q_
                               int64_t head_dim, int64_t block_size, int64_t table_width, int64_t chunk_tokens) {
     PrefillPlan p{};
     const int64_t group = q_heads / kv_heads;
-    // MFMA tiles for head_dim 128 and 256, and for narrower multiples of 8
-    // padded to 128 in LDS (zero dims add nothing to the scores and give zero
+    // MFMA tiles for every multiple of 8 up to 256: the 128 shape for head
+    // dims up to 128, the 256 shape above; dims below the shape's are padded
+    // with zeros in LDS (zero dims add nothing to the scores and give zero
     // outputs).
-    const bool wide = head_dim == 256;
-    p.narrow = head_dim < 128;
+    const bool wide = head_dim > 128;
     p.hd = wide ? 256 : 128;
+    p.narrow = head_dim < p.hd;
     p.keys = wide ? PfShape<256>::kKeys : PfShape<128>::kKeys;
     const int rows = wide ? PfShape<256>::kRows : PfShape<128>::kRows;
-    p.mfma = group <= rows && (head_dim == 128 || wide || (head_dim % 8 == 0 && head_dim >= 8 && p.narrow));
+    p.mfma = group <= rows && head_dim % 8 == 0 && head_dim >= 8 && head_dim <= 256;
     if (!p.mfma) return p;
     p.qb = (int)(rows / group);
     const int64_t keys = p.keys;
@@ -1491,7 +1491,14 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
         };
         auto launch_type = [&](auto type_tag) {
             using T = decltype(type_tag);
-            if (p.hd == 256) {
+            if (p.hd == 256 && p.narrow) {
+                if (pages == kPagesPerTile)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true, 256>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true, 256>);
+                else
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, true, 256>,
+                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, true, 256>);
+            } else if (p.hd == 256) {
                 if (pages == kPagesPerTile)
                     launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 256>,
                                 paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 256>);

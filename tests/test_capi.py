@@ -141,7 +141,9 @@ def test_scatter_and_prefill_reject_bad_arguments(lib):
         1024 * 16 * 8 * (256 * 2 + 2 * 4) + 1024 * 4
     assert lib.prefill_workspace_size(8, 1024, 16, 8, 64, 256, 16, 0, ext.BF16) == \
         1024 * 16 * 8 * (128 * 2 + 2 * 4) + 1024 * 4
-    assert lib.prefill_workspace_size(8, 1024, 16, 8, 192, 256, 16, 0, ext.BF16) == 0  # scalar kernel, no split
+    assert lib.prefill_workspace_size(8, 1024, 16, 8, 192, 256, 16, 0, ext.BF16) == \
+        1024 * 16 * 8 * (256 * 2 + 2 * 4) + 1024 * 4
+    assert lib.prefill_workspace_size(8, 1024, 16, 8, 264, 256, 16, 0, ext.BF16) == 0  # scalar kernel, no split
     assert lib.prefill_workspace_size(8, 1024, 16, 8, 128, 256, 16, 0, 9) == 0  # no such type
     assert lib.prefill_workspace_size(8, 1 << 40, 1 << 30, 8, 128, 256, 16, 0, ext.BF16) == 0  # refused shape
     assert _status(lib, "mvme_paged_prefill_attention", 1, 1, 1, 1, 1, 1, 1, 1, 8, 1024, 16, 8, 128, 200, 256, 16,

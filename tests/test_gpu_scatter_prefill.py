@@ -293,11 +293,25 @@ def test_mfma_prefill_head_dim_256(block, chunk_tokens, dtype, heads, kv_heads):
     assert max_err(actual, c_oracle.paged_prefill(*args, block)) <= GATE[dtype]
 
 
-@pytest.mark.parametrize("head_dim,block,dtype", [(100, 16, torch.bfloat16), (192, 256, torch.float16),
-                                                  (12, 4, torch.float16)])
+@pytest.mark.parametrize("head_dim,block,chunk_tokens,dtype", [
+    (192, 256, 0, torch.float16), (136, 16, 256, torch.bfloat16), (248, 5, 0, torch.bfloat16),
+    (160, 64, 128, torch.float16),
+])
+def test_mfma_prefill_heads_between_128_and_256(head_dim, block, chunk_tokens, dtype):
+    """Multiples of 8 between 128 and 256 run the 256 tile shape with rows
+    zero-padded to 256 (whole-tile and per-row copies, with key splits)."""
+    args = _two_sequence_case(head_dim, 8, 4, block, dtype, seed=head_dim + block)
+    print(f"prefill D={head_dim} block={block} chunk={chunk_tokens} {dtype}", flush=True)
+    actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip", chunk_tokens=chunk_tokens)
+    assert max_err(actual, paged_oracle.paged_prefill_attention(*args, block, cast=False)) <= GATE[dtype]
+    assert max_err(actual, c_oracle.paged_prefill(*args, block)) <= GATE[dtype]
+
+
+@pytest.mark.parametrize("head_dim,block,dtype", [(100, 16, torch.bfloat16), (12, 4, torch.float16),
+                                                  (264, 16, torch.float16)])
 def test_generic_prefill_other_head_dims(head_dim, block, dtype):
-    """Head dims the MFMA kernel does not take (not a multiple of 8, or above
-    128 other than 256) run the one-wave-per-row kernel."""
+    """Head dims the MFMA kernel does not take (not a multiple of 8, or
+    above 256) run the one-wave-per-row kernel."""
     args = _two_sequence_case(head_dim, 8, 4, block, dtype, seed=head_dim)
     print(f"generic prefill D={head_dim} block={block} {dtype}", flush=True)
     actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip")
