@@ -378,7 +378,8 @@ class CpuLeg:
 # Other workloads of the path (reported under "extra").
 # ---------------------------------------------------------------------------
 
-EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "kv_scatter", "norm_rope", "after_attention")
+EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "prefill_shapes", "kv_scatter", "norm_rope",
+               "after_attention")
 
 
 def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, cpu,
@@ -393,6 +394,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra)
     if "prefill" in names:
         _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra)
+    if "prefill_shapes" in names:
+        _extra_prefill_shapes(torch, write_kv_cache_slots, paged_prefill_attention, workloads, dev, extra)
     if "kv_scatter" in names:
         _extra_kv_scatter(torch, write_kv_cache_slots, workloads, cpu, dev, extra)
     if "norm_rope" in names:
@@ -522,6 +525,36 @@ def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloa
         "algorithmic_bytes": kv_bytes, "roofline_bound_us": bound_s * 1e6,
         "frac_of_roofline_time": bound_s / per_call, "flops": flops, "priors": c["priors"],
         "max_abs_error": err}
+
+
+def _extra_prefill_shapes(torch, write_kv_cache_slots, paged_prefill_attention, workloads, dev, extra):
+    """The same kernels on larger chunked-prefill shapes (bf16, block 256,
+    Hq16/Hkv8/D128): how far the fraction of the MFMA peak rises once each CU
+    has more than one short item to run.  Outputs are checked against the
+    oracle by the GPU tests at smaller sizes, not here."""
+    shapes = (("8x512_priors_U0_3968", 8, 512, [2220, 601, 877, 1126, 1381, 3550, 2532, 347]),
+              ("32x256_priors_U0_3968", 32, 256, None),
+              ("4x4096_causal", 4, 4096, [0, 0, 0, 0]),
+              ("1x16384_causal", 1, 16384, [0]))
+    names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+    rows = {}
+    for name, seqs, new_tokens, priors in shapes:
+        c = workloads.chunked_prefill_case(device=dev, num_seqs=seqs, new_tokens=new_tokens, priors=priors)
+        write_kv_cache_slots(c["key_cache"], c["value_cache"], c["slot_mapping"], c["new_key"], c["new_value"],
+                             backend="hip", validate=False)
+        pargs = [c[n] for n in names]
+
+        def run(n=3):
+            for _ in range(n):
+                paged_prefill_attention(*pargs, 256, backend="hip", validate=False)
+        ms, _ = graph_time_ms(run, torch, calls_per_graph=3, replays=10, warmup=3)
+        per_call = ms / 3 * 1e-3
+        flops = workloads.prefill_flops(c["priors"], new_tokens=new_tokens)
+        rows[name] = {"us_per_call": per_call * 1e6, "TFLOPs": flops / per_call / 1e12,
+                      "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS, "flops": flops}
+        del c, pargs
+        torch.cuda.empty_cache()
+    extra["chunked_prefill_other_shapes_bf16"] = rows
 
 
 def _extra_kv_scatter(torch, write_kv_cache_slots, workloads, cpu, dev, extra):
