@@ -188,9 +188,6 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     const int start = part * a.partition;
     const int end = min(start + a.partition, len);
 
-    // Fused prologue (kernel argument, uniform): rows 0 .. G of a list --
-    // row 0 the kv head's new K (and V), rows 1 .. G the tile's query heads
-    // (mode 2) -- one row per kLpt lanes.
     static_assert(!PRO || (S::kLpt == S::kChunks && S::kLpt >= 2), "prologue needs head_dim 16/32/64/128/256");
     // Fused prologue, with no barrier: the wave whose iterations hold the new
     // position writes its K/V row (and waits for that store before it loads
