@@ -60,14 +60,9 @@ namespace {
 
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * kWave;
-constexpr int kPfNb = 2;                        // 16-row MFMA column blocks per wave
-constexpr int kPfRows = kPfWaves * kPfNb * 16;  // 256 query rows per work-group (32 per wave)
-constexpr int kPfStages = 4;                    // LDS ring of K/V tiles
-constexpr int kPfIpw = 16 / kPfWaves;           // 1 KiB copy instructions per wave per K (or V) tile
-constexpr int kPfKeys = 64;        // keys per LDS tile
-constexpr int kPfD = 128;
-constexpr int kRowBytes = kPfD * 2;             // 256-byte key row
-constexpr int kTileBytes = kPfKeys * kRowBytes;  // 16 KiB per K or V tile
+constexpr int kPfStages = 4;              // LDS ring of K/V tiles
+constexpr int kTileBytes = 16384;         // one K (or V) tile in LDS, every tile shape
+constexpr int kPfMaxKeys = 64;            // keys per tile, largest tile shape
 
 // Tile shape of the MFMA kernel by padded head dim: 128 (head_dim 128 and
 // narrower multiples of 8) or 256.  Every tile is 16 KiB of K (and of V) in
@@ -351,7 +346,7 @@ constexpr int kPagesPerTile = 2;
 struct PrefillLds {
     alignas(16) uint8_t k[kPfStages][kTileBytes];
     alignas(16) uint8_t v[kPfStages][kTileBytes];
-    alignas(16) float b[kPfStages][kPfKeys];
+    alignas(16) float b[kPfStages][kPfMaxKeys];
     alignas(16) int full[kPfStages][kPfWaves];
     uint64_t pick[kPfWaves];  // chunk choice: each wave's best (cost, candidate)
     // The walk's index (num_seqs <= 64): sequence s's metadata, item count
