@@ -313,6 +313,9 @@ class CpuLeg:
     def prefill(self, *args, **kwargs):
         return self.oracle.paged_prefill_attention(*args, **kwargs)
 
+    def dense_prefill(self, *args, **kwargs):
+        return self.oracle.prefill_attention(*args, **kwargs)
+
     def norm_rope_write_kv(self, *args, **kwargs):
         return self.oracle.qk_norm_rope_write_kv(*args, **kwargs)
 
@@ -378,8 +381,8 @@ class CpuLeg:
 # Other workloads of the path (reported under "extra").
 # ---------------------------------------------------------------------------
 
-EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "prefill_shapes", "kv_scatter", "norm_rope",
-               "after_attention")
+EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "prefill_shapes", "dense_prefill", "kv_scatter",
+               "norm_rope", "after_attention")
 
 
 def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, cpu,
@@ -396,6 +399,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra)
     if "prefill_shapes" in names:
         _extra_prefill_shapes(torch, write_kv_cache_slots, paged_prefill_attention, workloads, dev, extra)
+    if "dense_prefill" in names:
+        _extra_dense_prefill(torch, workloads, cpu, dev, extra)
     if "kv_scatter" in names:
         _extra_kv_scatter(torch, write_kv_cache_slots, workloads, cpu, dev, extra)
     if "norm_rope" in names:
@@ -555,6 +560,43 @@ def _extra_prefill_shapes(torch, write_kv_cache_slots, paged_prefill_attention, 
         del c, pargs
         torch.cuda.empty_cache()
     extra["chunked_prefill_other_shapes_bf16"] = rows
+
+
+def _extra_dense_prefill(torch, workloads, cpu, dev, extra):
+    """Dense causal suffix prefill (prefill_attention): the reference's
+    single-request path, Attention.forward passing transposed views of
+    [tokens, heads, head_dim] tensors (native_qwen3.py:137-140), bf16,
+    Hq16/Hkv8/D128.  Square prompts of 2048 and 8192 tokens (8192 is the
+    reference CUDA kernel's limit) and 512 tokens after 3584; the 2048-token
+    prompt is checked against the oracle."""
+    from mini_engine_hip.kernels.prefill import prefill_attention
+
+    shapes = (("square_2048", 0, 2048), ("square_8192", 0, 8192), ("suffix_512_after_3584", 3584, 512))
+    rows = {}
+    for name, start, tokens in shapes:
+        gen = torch.Generator().manual_seed(BASE_SEED + tokens + start)
+        context = start + tokens
+        q_rows = torch.randn(tokens, HQ, D, generator=gen).to(torch.bfloat16).to(dev)
+        k_rows = torch.randn(context, HKV, D, generator=gen).to(torch.bfloat16).to(dev)
+        v_rows = torch.randn(context, HKV, D, generator=gen).to(torch.bfloat16).to(dev)
+        q, k, v = (t.transpose(0, 1).unsqueeze(0) for t in (q_rows, k_rows, v_rows))
+        holder = {}
+
+        def run(n=3):
+            for _ in range(n):
+                holder["out"] = prefill_attention(q, k, v, "hip", query_start=start)
+        ms, _ = graph_time_ms(run, torch, calls_per_graph=3, replays=10, warmup=3)
+        per_call = ms / 3 * 1e-3
+        flops = workloads.prefill_flops([start], new_tokens=tokens)
+        row = {"us_per_call": per_call * 1e6, "TFLOPs": flops / per_call / 1e12,
+               "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS, "flops": flops}
+        if name == "square_2048":
+            row["max_abs_error"] = None if cpu is None else max_abs(
+                holder["out"], cpu.dense_prefill(q.cpu(), k.cpu(), v.cpu(), query_start=start, cast=False))
+        rows[name] = row
+        del q, k, v, q_rows, k_rows, v_rows, holder
+        torch.cuda.empty_cache()
+    extra["dense_prefill_bf16"] = rows
 
 
 def _extra_kv_scatter(torch, write_kv_cache_slots, workloads, cpu, dev, extra):

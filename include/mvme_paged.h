@@ -245,6 +245,44 @@ int mvme_paged_prefill_attention(void* out, const void* q,
                                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Bytes of device workspace mvme_prefill_attention needs (0 when no query
+ * block is split over key chunks); 0 also for shapes it rejects.  Pure host
+ * function.  Same layout as mvme_paged_prefill_workspace_size.
+ */
+size_t mvme_prefill_attention_workspace_size(int64_t batch, int64_t q_tokens, int64_t q_heads,
+                                             int64_t kv_heads, int64_t head_dim, int64_t query_start,
+                                             int dtype);
+
+/*
+ * Dense causal suffix attention: q [batch, q_heads, q_tokens, head_dim], key /
+ * value [batch, kv_heads, kv_tokens, head_dim] (the same strides), output
+ * [batch, q_heads, q_tokens, head_dim].  Query row t of batch entry b and
+ * head h attends keys [0, query_start + t] of entry b and kv head
+ * h / (q_heads / kv_heads); 0 <= query_start, query_start + q_tokens <=
+ * kv_tokens, query_start + q_tokens <= 1,048,576.  Strides are in elements
+ * (batch, head, token; the head_dim dimension is dense), so views such as
+ * the transposes of [tokens, heads, head_dim] tensors need no copy.  For
+ * head dims that are multiples of 8 up to 256 (the MFMA path) every pointer
+ * must be 16-byte aligned and every stride a multiple of 8 elements; other
+ * head dims (up to 1024) need 2-byte alignment.  workspace: at least
+ * mvme_prefill_attention_workspace_size(...) bytes (may be NULL when 0).
+ * Runs the paged prefill kernels with each batch entry as one sequence whose
+ * keys are a single page.
+ * Replaces: causal_prefill_suffix_cuda / causal_prefill_kernel
+ *   (mini_engine/kernels/csrc/prefill.cu:15-98), bound as
+ *   extension.causal_prefill_suffix and causal_prefill
+ *   (csrc/bindings.cpp:217-218) and called from prefill_attention
+ *   (mini_engine/kernels/prefill.py:8-41, backend "cuda").
+ */
+int mvme_prefill_attention(void* out, const void* q, const void* key, const void* value,
+                           int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t q_tokens,
+                           int64_t kv_tokens, int64_t head_dim, int64_t query_start,
+                           int64_t q_batch_stride, int64_t q_head_stride, int64_t q_token_stride,
+                           int64_t kv_batch_stride, int64_t kv_head_stride, int64_t kv_token_stride,
+                           int64_t out_batch_stride, int64_t out_head_stride, int64_t out_token_stride,
+                           int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Fused per-head q/k RMSNorm + rotary embedding + KV page write (the step
  * before paged attention).  For every token t:
  *   q_out[t, h]             = rope(rmsnorm(q[t, h], q_weight))  (h < q_heads)

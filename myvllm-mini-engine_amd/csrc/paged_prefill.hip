@@ -51,6 +51,12 @@
 //
 // Generic path (any D <= 1024, any G): one wave per (query row, head),
 // online softmax over 64-key tiles, fp32 throughout.
+//
+// Dense mode (the dense suffix prefill of [B, H, T, D] tensors, at the end of
+// this file): the same kernels with batch entry b as sequence b, whose keys
+// are one page read through explicit strides, and no metadata arrays.  In
+// the MFMA kernel it is a template flag, so the paged instantiations keep
+// their code.
 #include "mvme_common.h"
 
 #include <algorithm>
@@ -122,7 +128,26 @@ struct PrefillArgs {
     int block_shift;  // log2(block_size) when a power of two, else -1
     int table_width;
     float scale_log2;
+    // Memory layout.  Key row k of page p, kv head h starts at byte
+    // p*kv_page_bytes + (k mod block_size)*kv_row_bytes + h*kv_head_bytes of
+    // the K (and V) base.  Query / output row (packed row r of sequence s,
+    // head h) starts at element s*x_seq + r*x_tok + h*x_head.
+    int64_t kv_page_bytes, kv_row_bytes, kv_head_bytes;
+    int64_t q_seq, q_tok, q_head;
+    int64_t o_seq, o_tok, o_head;
+    // Dense mode (tables == nullptr): every sequence has dense_tokens queries
+    // starting at position dense_start and context dense_start +
+    // dense_tokens; sequence s owns packed rows [s*dense_tokens, (s+1)*dense_tokens)
+    // and its keys are page s.  The metadata arrays are not read.
+    int dense_tokens;
+    int dense_start;
 };
+
+// Sequence of a packed row in dense mode (0 otherwise: the layouts of the
+// paged mode have no per-sequence term).
+__device__ inline int64_t dense_seq(const PrefillArgs& a, int64_t row) {
+    return a.dense_tokens > 0 ? row / a.dense_tokens : 0;
+}
 
 // Keys a query block [q0, q0+qb) of sequence s needs: [0, kv_end).
 __device__ inline int64_t block_kv_end(const PrefillArgs& a, int64_t start, int64_t ctx, int64_t qlen, int64_t q0) {
@@ -183,9 +208,15 @@ struct SeqMeta {
 // Offsets are clamped to the packed rows, so that metadata that is not
 // monotone (unchecked in trusted mode) can neither send a write past the
 // output nor make a lookup loop over an absurd number of query blocks.
+template <bool DENSE>
 __device__ inline SeqMeta load_meta(const PrefillArgs& a, int s) {
     SeqMeta m{0, 0, 0, 0};
-    if (s < a.num_seqs) {
+    if (DENSE && s < a.num_seqs) {
+        m.row0 = (int64_t)s * a.dense_tokens;
+        m.n = a.dense_tokens;
+        m.start = a.dense_start;
+        m.ctx = (int64_t)a.dense_start + a.dense_tokens;
+    } else if (!DENSE && s < a.num_seqs) {
         const int64_t lo = min(max(a.cu[s], (int64_t)0), a.total_tokens);
         const int64_t hi = min(max(a.cu[s + 1], lo), a.total_tokens);
         m.row0 = lo;
@@ -202,13 +233,14 @@ __device__ inline SeqMeta load_meta(const PrefillArgs& a, int s) {
 // counts its items, a wave prefix sum locates the sequence, the lane that
 // owns it hands its metadata over by shuffles, and that one sequence's query
 // blocks are walked.  Every wave of the work-group computes the same answer.
+template <bool DENSE>
 __device__ inline bool find_item(const PrefillArgs& a, int chunk_len, int item, PrefillItem& it,
                                  int* total_items = nullptr, const SeqMeta* first = nullptr) {
     const int lane = __lane_id();
     int base = 0;
     bool found = false;
     for (int s0 = 0; s0 < a.num_seqs; s0 += kWave) {
-        const SeqMeta m = (first && s0 == 0) ? *first : load_meta(a, s0 + lane);
+        const SeqMeta m = (first && s0 == 0) ? *first : load_meta<DENSE>(a, s0 + lane);
         const int64_t row0 = m.row0, n = m.n, start = m.start, ctx = m.ctx;
         const int cnt = seq_items(a, chunk_len, n, start, ctx);
         const int incl = wave_incl_scan(cnt);
@@ -427,7 +459,7 @@ __device__ inline bool find_item_indexed(const PrefillArgs& a, int chunk_len, in
 // zero-padded to HD in LDS (the copies skip the padded 16-byte chunks,
 // which stay zero), the queries' padded dims are zero, and only head_dim
 // output dims are stored.
-template <typename T, int PAGES, bool NARROW, int HD>
+template <typename T, int PAGES, bool NARROW, int HD, bool DENSE>
 __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a, const PrefillItem& item,
                                                             PrefillLds& lds) {
     using SH = PfShape<HD>;
@@ -460,7 +492,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     // [-1, cap] keeps every row's validity and its position in 32 bits.
     const int start = __builtin_amdgcn_readfirstlane(
         (int)(item.start < -1 ? -1 : (item.start > cap ? (int64_t)cap : item.start)));
-    const int64_t* table = a.tables + (int64_t)seq * a.table_width;
+    // Dense mode has no table: every key of sequence seq is in page seq.
+    constexpr bool ident = DENSE;
+    const int64_t* table = ident ? nullptr : a.tables + (int64_t)seq * a.table_width;
     const int kv_end = (int)kv_end64;
     const int chunk_len = __builtin_amdgcn_readfirstlane(item.chunk_len);
     const int chunk_start = chunk * chunk_len;
@@ -540,10 +574,13 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     // instructions j = SH::kIpw*w + i, each covering key rows 4j..4j+3 (lane ->
     // row 4j + lane/16, LDS slot lane%16 = global chunk (lane%16)^(row&15) for
     // K, (lane%16)^(2*row&15) for V).
-    const int64_t row_bytes_g = (int64_t)a.kv_heads * hd * 2;
-    const int64_t page_bytes_g = (int64_t)a.block_size * row_bytes_g;
-    const uint8_t* kcache = static_cast<const uint8_t*>(a.key_cache) + (int64_t)kvh * hd * 2;
-    const uint8_t* vcache = static_cast<const uint8_t*>(a.value_cache) + (int64_t)kvh * hd * 2;
+    // Paged mode: the cache layout [pages, block_size, kv_heads, hd] (the
+    // strides follow from the shapes, nothing more is held in registers).
+    const int64_t row_bytes_g = DENSE ? a.kv_row_bytes : (int64_t)a.kv_heads * hd * 2;
+    const int64_t page_bytes_g = DENSE ? a.kv_page_bytes : (int64_t)a.block_size * row_bytes_g;
+    const int64_t head_bytes_g = DENSE ? a.kv_head_bytes : (int64_t)hd * 2;
+    const uint8_t* kcache = static_cast<const uint8_t*>(a.key_cache) + kvh * head_bytes_g;
+    const uint8_t* vcache = static_cast<const uint8_t*>(a.value_cache) + kvh * head_bytes_g;
     const int bs_shift = a.block_shift;
     const int lrow = lane / SH::kChunks;  // row inside the instruction's rows
     const int lslot = lane % SH::kChunks;  // LDS slot of the lane's 16 bytes in that row
@@ -566,7 +603,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     auto page_at = [&](int key) -> int {
         const int kc = key < cap ? key : cap - 1;
         const int idx = bs_shift >= 0 ? kc >> bs_shift : kc / a.block_size;
-        const int64_t page = ctable[idx];
+        const int64_t page = ident ? seq : ctable[idx];
         return (key < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
     };
     // Page-per-tile mode: the page ids of a window of 64 consecutive tiles,
@@ -583,7 +620,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     auto window_pages = [&](int base) -> int64_t {
         const int key0 = (base + lane) * SH::kKeys;
         int64_t raw = -1;
-        if (key0 < chunk_end) raw = table[key0 >> bs_shift];
+        if (key0 < chunk_end) raw = ident ? seq : table[key0 >> bs_shift];
         return raw;
     };
     auto page_of_tile = [&](int tile) -> int {
@@ -662,7 +699,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     u32x4 qop[SH::kNb][SH::kDc];
 #pragma unroll
     for (int nb = 0; nb < SH::kNb; ++nb) {
-        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + ((row0 + qi[nb]) * a.q_heads + head[nb]) * hd;
+        const uint16_t* qrow = static_cast<const uint16_t*>(a.q) +
+                               (DENSE ? seq * a.q_seq + (row0 + qi[nb]) * a.q_tok + head[nb] * a.q_head
+                                      : ((row0 + qi[nb]) * a.q_heads + head[nb]) * hd);
 #pragma unroll
         for (int dc = 0; dc < SH::kDc; ++dc) {
             qop[nb][dc] = u32x4{0u, 0u, 0u, 0u};
@@ -670,6 +709,13 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 qop[nb][dc] = *reinterpret_cast<const u32x4*>(qrow + 32 * dc + 8 * lg);
         }
     }
+
+    // Dense mode: output row offsets (elements), formed here so that the
+    // layout's strides are not held in scalar registers across the tile loop.
+    int64_t out_off[SH::kNb];
+#pragma unroll
+    for (int nb = 0; nb < SH::kNb; ++nb)
+        out_off[nb] = DENSE ? seq * a.o_seq + (row0 + qi[nb]) * a.o_tok + head[nb] * a.o_head : 0;
 
     // Prologue: only the first tile in flight, so the first products wait
     // for the queries and one tile; the pairs that follow are (t, t+1) with
@@ -680,7 +726,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             // the first barrier, so nothing waits for it (or for the queries)
             // before these copies go out.
             const int key0 = t_begin * SH::kKeys;
-            const int64_t page = ctable[key0 >> bs_shift];
+            const int64_t page = ident ? seq : ctable[key0 >> bs_shift];
             const int pg = (key0 < chunk_end && page >= 0 && page < a.num_blocks) ? (int)page : -1;
 #pragma unroll
             for (int i = 0; i < SH::kIpw; ++i) pg_next[i] = pg;
@@ -903,7 +949,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         const int64_t rowid = (row0 + qi[nb]) * a.q_heads + head[nb];
         if (nchunks == 1) {
             const float inv = (row_ok[nb] && l_row > 0.f) ? __builtin_amdgcn_rcpf(l_row) : 0.f;
-            uint16_t* orow = static_cast<uint16_t*>(a.out) + rowid * hd;
+            uint16_t* orow = static_cast<uint16_t*>(a.out) + (DENSE ? out_off[nb] : rowid * hd);
 #pragma unroll
             for (int dt = 0; dt < SH::kDt; ++dt) {
                 const u32x2 w = {T::pack(o[nb][dt][0] * inv, o[nb][dt][1] * inv),
@@ -957,7 +1003,7 @@ constexpr float kItemFixedTiles = 2.5f;  // in 64-key tiles
 constexpr int kChoiceCands = 128;
 constexpr int kChoiceSlices = kPfThreads / kChoiceCands;
 
-template <int KEYS>
+template <int KEYS, bool DENSE>
 __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta& first) {
     constexpr float kFixed = kItemFixedTiles * 64.f / KEYS;  // an item's fixed cost in tiles of KEYS keys
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -973,7 +1019,7 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
         int blk = 0;  // query blocks of the sequences before (uniform)
         for (int s0 = 0; s0 < a.num_seqs; s0 += kWave) {
             // One sequence's metadata per lane, then every lane walks them all.
-            const SeqMeta m = s0 == 0 ? first : load_meta(a, s0 + lane);
+            const SeqMeta m = s0 == 0 ? first : load_meta<DENSE>(a, s0 + lane);
             const int64_t n = m.n, start = m.start, ctx = m.ctx;
             const int cnt = min(kWave, a.num_seqs - s0);
             for (int j = 0; j < cnt; ++j) {
@@ -1029,7 +1075,7 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
 // true: one work-group per CU slot, each walking items idx, idx +
 // item_stride, ... below the item count (a separate instantiation, so that
 // the one-item kernel keeps its register allocation).
-template <typename T, int PAGES, bool WALK, bool NARROW, int HD>
+template <typename T, int PAGES, bool WALK, bool NARROW, int HD, bool DENSE>
 __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) PrefillLds lds;
     if constexpr (NARROW && PAGES == kPagesPerTile) {
@@ -1043,8 +1089,8 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
     }
     if constexpr (!WALK) {
         PrefillItem item;
-        if (!find_item(a, a.chunk, blockIdx.x / a.kv_heads, item)) return;
-        prefill_item<T, PAGES, NARROW, HD>(a, item, lds);
+        if (!find_item<DENSE>(a, a.chunk, blockIdx.x / a.kv_heads, item)) return;
+        prefill_item<T, PAGES, NARROW, HD, DENSE>(a, item, lds);
     } else {
         // The first lookup also counts the items, so that the walk ends
         // without a lookup past the end.
@@ -1058,32 +1104,32 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
         int chunk_len = a.chunk;
         bool ok = false;
         if (indexed) {
-            const SeqMeta m = load_meta(a, (int)(threadIdx.x & (kWave - 1)));
+            const SeqMeta m = load_meta<DENSE>(a, (int)(threadIdx.x & (kWave - 1)));
             int cnt, incl;
             total = walk_index(a, chunk_len, m, lds, cnt, incl);
             if (a.chunk_choice && total > a.item_stride) {
                 // More than one round of items: the lengths decide the chunk.
-                chunk_len = choose_chunk<PfShape<HD>::kKeys>(a, lds, m);
+                chunk_len = choose_chunk<PfShape<HD>::kKeys, DENSE>(a, lds, m);
                 total = walk_index(a, chunk_len, m, lds, cnt, incl);
             }
             // The first lookup uses this wave's own copy of the index; wave 0's
             // LDS copy serves the later ones (after the barrier between items).
             ok = find_item_lanes(a, chunk_len, total, m, cnt, incl, idx, item);
         } else {
-            ok = find_item(a, chunk_len, idx, item, &total);
+            ok = find_item<DENSE>(a, chunk_len, idx, item, &total);
             if (a.chunk_choice && total > a.item_stride) {
-                const SeqMeta m = load_meta(a, (int)(threadIdx.x & (kWave - 1)));
-                chunk_len = choose_chunk<PfShape<HD>::kKeys>(a, lds, m);
-                ok = find_item(a, chunk_len, idx, item, &total);
+                const SeqMeta m = load_meta<DENSE>(a, (int)(threadIdx.x & (kWave - 1)));
+                chunk_len = choose_chunk<PfShape<HD>::kKeys, DENSE>(a, lds, m);
+                ok = find_item<DENSE>(a, chunk_len, idx, item, &total);
             }
         }
         while (ok) {
-            prefill_item<T, PAGES, NARROW, HD>(a, item, lds);
+            prefill_item<T, PAGES, NARROW, HD, DENSE>(a, item, lds);
             idx += a.item_stride;
             if (idx >= total) break;
             __syncthreads();  // every wave is done with the LDS ring before the next item refills it
             ok = indexed ? find_item_indexed(a, chunk_len, total, lds, idx, item)
-                         : find_item(a, chunk_len, idx, item);
+                         : find_item<DENSE>(a, chunk_len, idx, item);
         }
     }
 }
@@ -1172,7 +1218,9 @@ __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(Pref
         const float inv = sum > 0.f ? 1.f / sum : 0.f;
         const u32x4 wv = {T::pack(acc[0] * inv, acc[1] * inv), T::pack(acc[2] * inv, acc[3] * inv),
                           T::pack(acc[4] * inv, acc[5] * inv), T::pack(acc[6] * inv, acc[7] * inv)};
-        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.out) + (token * a.q_heads + head) * a.head_dim + d0) = wv;
+        uint16_t* orow =
+            static_cast<uint16_t*>(a.out) + dense_seq(a, token) * a.o_seq + token * a.o_tok + head * a.o_head;
+        *reinterpret_cast<u32x4*>(orow + d0) = wv;
     }
 }
 
@@ -1195,30 +1243,41 @@ __global__ __launch_bounds__(kWave) void paged_prefill_generic_kernel(PrefillArg
     const int head = blockIdx.y;
     const int lane = threadIdx.x;
     const int D = a.head_dim;
-    uint16_t* orow = static_cast<uint16_t*>(a.out) + (token * a.q_heads + head) * D;
+    const int64_t dseq = dense_seq(a, token);
+    uint16_t* orow = static_cast<uint16_t*>(a.out) + dseq * a.o_seq + token * a.o_tok + head * a.o_head;
 
-    // Sequence owning this packed row (cu is monotone).
-    int lo = 0, hi = a.num_seqs;
-    while (lo < hi) {
-        const int mid = (lo + hi) / 2;
-        if (a.cu[mid + 1] <= token) lo = mid + 1;
-        else hi = mid;
-    }
-    bool ok = lo < a.num_seqs && token >= a.cu[lo];
+    // Sequence owning this packed row (cu is monotone; dense mode: every
+    // sequence has dense_tokens rows).
+    int lo = 0;
+    bool ok;
     int64_t pos = 0;
     const int64_t cap = (int64_t)a.table_width * a.block_size;
-    if (ok) {
-        pos = a.starts[lo] + token - a.cu[lo];
-        ok = a.starts[lo] >= 0 && pos < a.lens[lo] && pos < cap;
+    if (a.dense_tokens > 0) {
+        lo = (int)dseq;
+        pos = a.dense_start + token - dseq * a.dense_tokens;
+        ok = lo < a.num_seqs && pos < cap;
+    } else {
+        int hi = a.num_seqs;
+        while (lo < hi) {
+            const int mid = (lo + hi) / 2;
+            if (a.cu[mid + 1] <= token) lo = mid + 1;
+            else hi = mid;
+        }
+        ok = lo < a.num_seqs && token >= a.cu[lo];
+        if (ok) {
+            pos = a.starts[lo] + token - a.cu[lo];
+            ok = a.starts[lo] >= 0 && pos < a.lens[lo] && pos < cap;
+        }
     }
     if (!ok) {
         for (int d = lane; d < D; d += kWave) orow[d] = 0;
         return;
     }
     const int kvh = head / a.group;
-    const int64_t* table = a.tables + (int64_t)lo * a.table_width;
-    const int64_t row_elems = (int64_t)a.kv_heads * D;
-    const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + (token * a.q_heads + head) * D;
+    const bool ident = a.tables == nullptr;
+    const int64_t* table = ident ? nullptr : a.tables + (int64_t)lo * a.table_width;
+    const int64_t page_elems = a.kv_page_bytes / 2, row_elems = a.kv_row_bytes / 2;
+    const uint16_t* qrow = static_cast<const uint16_t*>(a.q) + dseq * a.q_seq + token * a.q_tok + head * a.q_head;
     for (int d = lane; d < D; d += kWave) sm_q[d] = elem_to_float<T>(qrow[d]);
     __syncthreads();
 
@@ -1227,15 +1286,15 @@ __global__ __launch_bounds__(kWave) void paged_prefill_generic_kernel(PrefillArg
 #pragma unroll
     for (int i = 0; i < kPer; ++i) acc[i] = 0.f;
     float m_run = kNegInf, l_run = 0.f;
-    const uint16_t* kcache = static_cast<const uint16_t*>(a.key_cache) + (int64_t)kvh * D;
-    const uint16_t* vcache = static_cast<const uint16_t*>(a.value_cache) + (int64_t)kvh * D;
+    const uint16_t* kcache = static_cast<const uint16_t*>(a.key_cache) + kvh * (a.kv_head_bytes / 2);
+    const uint16_t* vcache = static_cast<const uint16_t*>(a.value_cache) + kvh * (a.kv_head_bytes / 2);
 
     for (int64_t k0 = 0; k0 <= pos; k0 += kWave) {
         const int64_t key = k0 + lane;
         int64_t page = -1;
-        if (key <= pos) page = table[key / a.block_size];
+        if (key <= pos) page = ident ? lo : table[key / a.block_size];
         const bool kv_ok = page >= 0 && page < a.num_blocks;
-        const int64_t off = kv_ok ? (page * a.block_size + key % a.block_size) * row_elems : -1;
+        const int64_t off = kv_ok ? page * page_elems + (key % a.block_size) * row_elems : -1;
         float s = kNegInf;
         if (kv_ok) {
             const uint16_t* krow = kcache + off;
@@ -1374,6 +1433,131 @@ PrefillWorkspace prefill_workspace_layout(int64_t rows, int64_t max_chunks, int6
     return w;
 }
 
+// Launches the attention kernel (and the merge of split query blocks) for
+// arguments whose layout and metadata fields are filled in; `need` is the
+// plan's workspace size, already checked against the caller's buffer.
+int launch_prefill(PrefillArgs a, const PrefillPlan& p, int64_t total_tokens, int64_t chunk_tokens, int dtype,
+                   size_t need, void* workspace, hipStream_t s, const char* what) {
+    const int64_t q_heads = a.q_heads, kv_heads = a.kv_heads, table_width = a.table_width;
+    if (p.mfma) {
+        if (table_width * a.block_size > 2147483647)
+            return fail(MVME_EINVAL, "paged prefill table capacity exceeds 2^31 tokens");
+        a.qb = p.qb;
+        a.part_dim = p.hd;
+        a.chunk = p.chunk;
+        a.max_chunks = p.max_chunks;
+        a.ws_rows = total_tokens * q_heads;
+        a.total_tokens = total_tokens;
+        a.chunk_choice = chunk_tokens <= 0 ? 1 : 0;
+        if (need > 0) {
+            const PrefillWorkspace w = prefill_workspace_layout(total_tokens * q_heads, p.max_chunks, total_tokens,
+                                                                dtype, p.hd);
+            a.ws_o = workspace;
+            a.ws_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + w.ml_offset);
+            a.ws_tok = reinterpret_cast<int*>(static_cast<uint8_t*>(workspace) + w.tok_offset);
+        }
+        // The item count depends on lengths that stay on the device, so the
+        // grid is sized from a bound.  With key splitting that bound is loose
+        // (every block counted with the most chunks) and surplus work-groups
+        // would queue behind the real ones (one work-group fits a CU): there
+        // the grid is one work-group per CU slot, each walking its items.
+        int64_t item_slots = p.items_bound;
+        a.item_stride = 0;
+        if (p.max_chunks > 1) {
+            const int64_t slots = std::max<int64_t>(1, kPrefillCUs / kv_heads);
+            if (p.items_bound > slots) {
+                item_slots = slots;
+                a.item_stride = (int)slots;
+            }
+        }
+        const int64_t groups = item_slots * kv_heads;
+        if (groups > 2147483647) return fail(MVME_EINVAL, "paged prefill grid too large");
+        // Whole-tile pages: a tile lies in one page (power-of-two blocks of at
+        // least a tile's keys) and per-lane offsets inside a tile fit 32 bits.
+        const bool tile_pages = a.block_shift >= 0 && a.block_size >= p.keys &&
+                                a.kv_row_bytes * p.keys < (int64_t(1) << 31);
+        const int64_t block_size = a.block_size;
+        const bool dense = a.tables == nullptr;
+        if (dense && !tile_pages) return fail(MVME_EINVAL, "prefill key/value token stride too large");
+        int pages = tile_pages ? kPagesPerTile : (block_size % 4 == 0 ? kPagesPerRows : kPagesPerLane);
+        if (p.narrow && pages == kPagesPerRows) pages = kPagesPerLane;  // no narrow instantiation of that mode
+        const dim3 grid((unsigned)groups), block(kPfThreads);
+        auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, s, a); };
+        auto launch_walk = [&](auto one, auto walk) {
+            if (a.item_stride > 0) launch(walk);
+            else launch(one);
+        };
+        auto launch_type = [&](auto type_tag) {
+            using T = decltype(type_tag);
+            if (dense) {
+                // Dense mode: one power-of-two page per sequence, whole-tile copies.
+                if (p.hd == 256 && p.narrow)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true, 256, true>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true, 256, true>);
+                else if (p.hd == 256)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 256, true>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 256, true>);
+                else if (p.narrow)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true, 128, true>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true, 128, true>);
+                else
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 128, true>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 128, true>);
+            } else if (p.hd == 256 && p.narrow) {
+                if (pages == kPagesPerTile)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true, 256, false>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true, 256, false>);
+                else
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, true, 256, false>,
+                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, true, 256, false>);
+            } else if (p.hd == 256) {
+                if (pages == kPagesPerTile)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 256, false>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 256, false>);
+                else if (pages == kPagesPerRows)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerRows, false, false, 256, false>,
+                                paged_prefill_mfma_kernel<T, kPagesPerRows, true, false, 256, false>);
+                else
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, false, 256, false>,
+                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, false, 256, false>);
+            } else if (p.narrow) {
+                if (pages == kPagesPerTile)
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true, 128, false>,
+                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true, 128, false>);
+                else
+                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, true, 128, false>,
+                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, true, 128, false>);
+            } else if (pages == kPagesPerTile) {
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 128, false>,
+                            paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 128, false>);
+            } else if (pages == kPagesPerRows) {
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerRows, false, false, 128, false>,
+                            paged_prefill_mfma_kernel<T, kPagesPerRows, true, false, 128, false>);
+            } else {
+                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, false, 128, false>,
+                            paged_prefill_mfma_kernel<T, kPagesPerLane, true, false, 128, false>);
+            }
+        };
+        if (dtype == MVME_FP16) launch_type(Half{});
+        else launch_type(BFloat16{});
+        if (p.max_chunks > 1) {
+            const dim3 grid((unsigned)total_tokens);
+            if (dtype == MVME_FP16)
+                hipLaunchKernelGGL((paged_prefill_merge_kernel<Half>), grid, dim3(kMergeThreads), 0, s, a);
+            else
+                hipLaunchKernelGGL((paged_prefill_merge_kernel<BFloat16>), grid, dim3(kMergeThreads), 0, s, a);
+        }
+    } else {
+        if (q_heads > 65535) return fail(MVME_EINVAL, "paged prefill grid too large");
+        const dim3 grid((unsigned)total_tokens, (unsigned)q_heads);
+        if (dtype == MVME_FP16)
+            hipLaunchKernelGGL((paged_prefill_generic_kernel<Half>), grid, dim3(kWave), 0, s, a);
+        else
+            hipLaunchKernelGGL((paged_prefill_generic_kernel<BFloat16>), grid, dim3(kWave), 0, s, a);
+    }
+    return check_launch(what);
+}
+
 }  // namespace
 }  // namespace mvme
 
@@ -1438,105 +1622,133 @@ extern "C" int mvme_paged_prefill_attention(void* out, const void* q, const void
     a.block_shift = (block_size & (block_size - 1)) == 0 ? __builtin_ctzll((unsigned long long)block_size) : -1;
     a.table_width = (int)table_width;
     a.scale_log2 = kLog2e / sqrtf((float)head_dim);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    if (p.mfma) {
-        if (table_width * block_size > 2147483647)
-            return fail(MVME_EINVAL, "paged prefill table capacity exceeds 2^31 tokens");
-        a.qb = p.qb;
-        a.part_dim = p.hd;
-        a.chunk = p.chunk;
-        a.max_chunks = p.max_chunks;
-        a.ws_rows = total_tokens * q_heads;
-        a.total_tokens = total_tokens;
-        a.chunk_choice = chunk_tokens <= 0 ? 1 : 0;
-        if (need > 0) {
-            const PrefillWorkspace w = prefill_workspace_layout(total_tokens * q_heads, p.max_chunks, total_tokens,
-                                                                dtype, p.hd);
-            a.ws_o = workspace;
-            a.ws_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + w.ml_offset);
-            a.ws_tok = reinterpret_cast<int*>(static_cast<uint8_t*>(workspace) + w.tok_offset);
-        }
-        // The item count depends on lengths that stay on the device, so the
-        // grid is sized from a bound.  With key splitting that bound is loose
-        // (every block counted with the most chunks) and surplus work-groups
-        // would queue behind the real ones (one work-group fits a CU): there
-        // the grid is one work-group per CU slot, each walking its items.
-        int64_t item_slots = p.items_bound;
-        a.item_stride = 0;
-        if (p.max_chunks > 1) {
-            const int64_t slots = std::max<int64_t>(1, kPrefillCUs / kv_heads);
-            if (p.items_bound > slots) {
-                item_slots = slots;
-                a.item_stride = (int)slots;
-            }
-        }
-        const int64_t groups = item_slots * kv_heads;
-        if (groups > 2147483647) return fail(MVME_EINVAL, "paged prefill grid too large");
-        // Whole-tile pages: a tile lies in one page (power-of-two blocks of at
-        // least a tile's keys) and per-lane offsets inside a tile fit 32 bits.
-        const bool tile_pages = a.block_shift >= 0 && block_size >= p.keys &&
-                                kv_heads * head_dim * 2 * p.keys < (int64_t(1) << 31);
-        int pages = tile_pages ? kPagesPerTile : (block_size % 4 == 0 ? kPagesPerRows : kPagesPerLane);
-        if (p.narrow && pages == kPagesPerRows) pages = kPagesPerLane;  // no narrow instantiation of that mode
-        const dim3 grid((unsigned)groups), block(kPfThreads);
-        auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, s, a); };
-        auto launch_walk = [&](auto one, auto walk) {
-            if (a.item_stride > 0) launch(walk);
-            else launch(one);
-        };
-        auto launch_type = [&](auto type_tag) {
-            using T = decltype(type_tag);
-            if (p.hd == 256 && p.narrow) {
-                if (pages == kPagesPerTile)
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true, 256>,
-                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true, 256>);
-                else
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, true, 256>,
-                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, true, 256>);
-            } else if (p.hd == 256) {
-                if (pages == kPagesPerTile)
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 256>,
-                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 256>);
-                else if (pages == kPagesPerRows)
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerRows, false, false, 256>,
-                                paged_prefill_mfma_kernel<T, kPagesPerRows, true, false, 256>);
-                else
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, false, 256>,
-                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, false, 256>);
-            } else if (p.narrow) {
-                if (pages == kPagesPerTile)
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, true, 128>,
-                                paged_prefill_mfma_kernel<T, kPagesPerTile, true, true, 128>);
-                else
-                    launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, true, 128>,
-                                paged_prefill_mfma_kernel<T, kPagesPerLane, true, true, 128>);
-            } else if (pages == kPagesPerTile) {
-                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerTile, false, false, 128>,
-                            paged_prefill_mfma_kernel<T, kPagesPerTile, true, false, 128>);
-            } else if (pages == kPagesPerRows) {
-                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerRows, false, false, 128>,
-                            paged_prefill_mfma_kernel<T, kPagesPerRows, true, false, 128>);
-            } else {
-                launch_walk(paged_prefill_mfma_kernel<T, kPagesPerLane, false, false, 128>,
-                            paged_prefill_mfma_kernel<T, kPagesPerLane, true, false, 128>);
-            }
-        };
-        if (dtype == MVME_FP16) launch_type(Half{});
-        else launch_type(BFloat16{});
-        if (p.max_chunks > 1) {
-            const dim3 grid((unsigned)total_tokens);
-            if (dtype == MVME_FP16)
-                hipLaunchKernelGGL((paged_prefill_merge_kernel<Half>), grid, dim3(kMergeThreads), 0, s, a);
-            else
-                hipLaunchKernelGGL((paged_prefill_merge_kernel<BFloat16>), grid, dim3(kMergeThreads), 0, s, a);
-        }
-    } else {
-        if (q_heads > 65535) return fail(MVME_EINVAL, "paged prefill grid too large");
-        const dim3 grid((unsigned)total_tokens, (unsigned)q_heads);
-        if (dtype == MVME_FP16)
-            hipLaunchKernelGGL((paged_prefill_generic_kernel<Half>), grid, dim3(kWave), 0, s, a);
-        else
-            hipLaunchKernelGGL((paged_prefill_generic_kernel<BFloat16>), grid, dim3(kWave), 0, s, a);
-    }
-    return check_launch("paged prefill");
+    // Paged layout: [pages, block_size, kv_heads, head_dim] caches, packed
+    // [tokens, q_heads, head_dim] queries and outputs.
+    a.kv_row_bytes = kv_heads * head_dim * 2;
+    a.kv_page_bytes = block_size * a.kv_row_bytes;
+    a.kv_head_bytes = head_dim * 2;
+    a.q_tok = a.o_tok = q_heads * head_dim;
+    a.q_head = a.o_head = head_dim;
+    return launch_prefill(a, p, total_tokens, chunk_tokens, dtype, need, workspace,
+                          static_cast<hipStream_t>(stream), "paged prefill");
+}
+
+// ---------------------------------------------------------------------------
+// Dense suffix prefill: q [B, Hq, T, D], k and v [B, Hkv, S, D], any strides
+// with a dense innermost dim; row (b, h, t) attends keys [0, query_start + t]
+// of batch entry b.  The paged kernels run in dense mode: batch entry b is
+// sequence b with T queries, its keys are one page (the entry itself, read
+// through the strides), and no metadata arrays exist.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kMaxDenseContext = 1048576;  // query_start + T
+
+// The one page holding a sequence's keys: a power of two >= the context and
+// >= a tile's keys, so that the whole-tile copy mode applies.
+int64_t dense_block(int64_t ctx) {
+    int64_t bs = 64;
+    while (bs < ctx) bs *= 2;
+    return bs;
+}
+
+bool dense_shapes_ok(int64_t batch, int64_t q_tokens, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                     int64_t query_start) {
+    return batch > 0 && q_tokens > 0 && q_heads > 0 && kv_heads > 0 && q_heads % kv_heads == 0 && head_dim > 0 &&
+           head_dim <= kGenMaxD && query_start >= 0 && query_start <= kMaxDenseContext &&
+           q_tokens <= kMaxDenseContext && query_start + q_tokens <= kMaxDenseContext &&
+           batch <= kMaxPrefillSeqs && batch * q_tokens <= kMaxPrefillRows / q_heads;
+}
+
+// Largest element offset a strided [n0, n1, n2, d] view can reach, plus the
+// intermediate products the kernels form (rows of every batch entry times
+// the token stride), kept below 2^60.
+bool strided_span_ok(int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t n2, int64_t s2, int64_t d) {
+    if (s0 < 0 || s1 < 0 || s2 < 0) return false;
+    const __int128 span = (__int128)n0 * s0 + (__int128)n0 * n2 * s2 + (__int128)n1 * s1 + d;
+    return span < ((__int128)1 << 60);
+}
+
+}  // namespace
+
+extern "C" size_t mvme_prefill_attention_workspace_size(int64_t batch, int64_t q_tokens, int64_t q_heads,
+                                                        int64_t kv_heads, int64_t head_dim, int64_t query_start,
+                                                        int dtype) {
+    if (!valid_dtype(dtype) || !dense_shapes_ok(batch, q_tokens, q_heads, kv_heads, head_dim, query_start))
+        return 0;
+    const int64_t rows = batch * q_tokens;
+    const PrefillPlan p = make_prefill_plan(batch, rows, q_heads, kv_heads, head_dim,
+                                            dense_block(query_start + q_tokens), 1, 0);
+    if (!p.mfma || p.max_chunks <= 1) return 0;
+    return prefill_workspace_layout(rows * q_heads, p.max_chunks, rows, dtype, p.hd).bytes;
+}
+
+extern "C" int mvme_prefill_attention(void* out, const void* q, const void* key, const void* value, int64_t batch,
+                                      int64_t q_heads, int64_t kv_heads, int64_t q_tokens, int64_t kv_tokens,
+                                      int64_t head_dim, int64_t query_start, int64_t q_batch_stride,
+                                      int64_t q_head_stride, int64_t q_token_stride, int64_t kv_batch_stride,
+                                      int64_t kv_head_stride, int64_t kv_token_stride, int64_t out_batch_stride,
+                                      int64_t out_head_stride, int64_t out_token_stride, int dtype, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+    if (!valid_dtype(dtype)) return fail(MVME_EINVAL, "prefill requires FP16/BF16");
+    if (batch <= 0 || head_dim <= 0 || kv_tokens <= 0) return fail(MVME_EINVAL, "prefill shape mismatch");
+    if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0) return fail(MVME_EINVAL, "prefill GQA mismatch");
+    if (head_dim > kGenMaxD) return fail(MVME_EINVAL, "prefill supports head_dim up to 1024");
+    if (query_start < 0 || q_tokens <= 0 || query_start > kv_tokens || q_tokens > kv_tokens - query_start)
+        return fail(MVME_EINVAL, "prefill query range exceeds KV sequence");
+    if (!dense_shapes_ok(batch, q_tokens, q_heads, kv_heads, head_dim, query_start))
+        return fail(MVME_EINVAL, "prefill context exceeds 1048576 tokens or too many rows");
+    if (!out || !q || !key || !value) return fail(MVME_EINVAL, "prefill received a null pointer");
+    if (!strided_span_ok(batch, q_batch_stride, q_heads, q_head_stride, q_tokens, q_token_stride, head_dim) ||
+        !strided_span_ok(batch, out_batch_stride, q_heads, out_head_stride, q_tokens, out_token_stride, head_dim) ||
+        !strided_span_ok(batch, kv_batch_stride, kv_heads, kv_head_stride, kv_tokens, kv_token_stride, head_dim))
+        return fail(MVME_EINVAL, "prefill strides out of range");
+    const int64_t ctx = query_start + q_tokens;
+    const int64_t bs = dense_block(ctx);
+    const int64_t rows = batch * q_tokens;
+    const PrefillPlan p = make_prefill_plan(batch, rows, q_heads, kv_heads, head_dim, bs, 1, 0);
+    // The MFMA path moves rows in 16-byte pieces (the generic kernel reads elements).
+    const int64_t align = p.mfma ? 16 : 2;
+    const int64_t stride_mult = align / 2;
+    for (const void* ptr : {static_cast<const void*>(out), q, key, value})
+        if (reinterpret_cast<uintptr_t>(ptr) % align != 0)
+            return fail(MVME_EINVAL, "prefill tensors must be " + std::to_string(align) + "-byte aligned");
+    for (int64_t st : {q_batch_stride, q_head_stride, q_token_stride, kv_batch_stride, kv_head_stride,
+                       kv_token_stride, out_batch_stride, out_head_stride, out_token_stride})
+        if (st % stride_mult != 0)
+            return fail(MVME_EINVAL, "prefill strides must be multiples of " + std::to_string(stride_mult) +
+                                         " elements");
+    const size_t need =
+        mvme_prefill_attention_workspace_size(batch, q_tokens, q_heads, kv_heads, head_dim, query_start, dtype);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need))
+        return fail(MVME_EWORKSPACE, "prefill workspace too small: need " + std::to_string(need) + " bytes, got " +
+                                         std::to_string(workspace_bytes));
+    PrefillArgs a{};
+    a.out = out;
+    a.q = q;
+    a.key_cache = key;
+    a.value_cache = value;
+    a.num_seqs = (int)batch;
+    a.q_heads = (int)q_heads;
+    a.kv_heads = (int)kv_heads;
+    a.group = (int)(q_heads / kv_heads);
+    a.head_dim = (int)head_dim;
+    a.num_blocks = batch;
+    a.block_size = (int)bs;
+    a.block_shift = __builtin_ctzll((unsigned long long)bs);
+    a.table_width = 1;
+    a.scale_log2 = kLog2e / sqrtf((float)head_dim);
+    a.dense_tokens = (int)q_tokens;
+    a.dense_start = (int)query_start;
+    a.kv_page_bytes = kv_batch_stride * 2;
+    a.kv_row_bytes = kv_token_stride * 2;
+    a.kv_head_bytes = kv_head_stride * 2;
+    // Packed row r = b*T + t: s*x_seq + r*x_tok = b*batch_stride + t*token_stride.
+    a.q_seq = q_batch_stride - q_tokens * q_token_stride;
+    a.q_tok = q_token_stride;
+    a.q_head = q_head_stride;
+    a.o_seq = out_batch_stride - q_tokens * out_token_stride;
+    a.o_tok = out_token_stride;
+    a.o_head = out_head_stride;
+    return launch_prefill(a, p, rows, 0, dtype, need, workspace, static_cast<hipStream_t>(stream), "prefill");
 }

@@ -43,6 +43,8 @@ SIGNATURES = {
     "mvme_paged_prefill_workspace_size": (_size, [_i64] * 8 + [_int]),
     "mvme_paged_prefill_attention": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                             _i64, _i64, _i64, _i64, _i64, _i64, _int, _vp, _size, _vp]),
+    "mvme_prefill_attention_workspace_size": (_size, [_i64] * 6 + [_int]),
+    "mvme_prefill_attention": (_int, [_vp, _vp, _vp, _vp] + [_i64] * 16 + [_int, _vp, _size, _vp]),
     "mvme_qk_norm_rope_write_kv": (_int, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp,
                                           _vp, _vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
                                           ctypes.c_float, _int, _vp]),
@@ -80,6 +82,9 @@ class HipLibrary:
 
     def prefill_workspace_size(self, *args) -> int:
         return int(self._lib.mvme_paged_prefill_workspace_size(*args))
+
+    def dense_prefill_workspace_size(self, *args) -> int:
+        return int(self._lib.mvme_prefill_attention_workspace_size(*args))
 
     def argmax_workspace_size(self, *args) -> int:
         return int(self._lib.mvme_greedy_argmax_workspace_size(*args))

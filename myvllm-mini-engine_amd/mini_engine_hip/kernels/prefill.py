@@ -1,10 +1,14 @@
-"""Ragged chunked paged prefill attention, ``backend="hip"``.
+"""Prefill attention, ``backend="hip"``: ragged chunked paged prefill and
+dense causal suffix prefill.
 
-Same signature, metadata contract and validation messages as the
-reference's ``paged_prefill_attention`` (mini_engine/kernels/prefill.py:61-131)
-and its native op (mini_engine/kernels/csrc/prefill.cu:200-240).  Packed
-queries read the paged KV cache directly; D=128 runs on bf16/fp16 MFMA tiles,
-other head sizes (up to 1024) on a generic HIP kernel.
+``paged_prefill_attention`` has the same signature, metadata contract and
+validation messages as the reference's (mini_engine/kernels/prefill.py:61-131)
+and its native op (mini_engine/kernels/csrc/prefill.cu:200-240): packed
+queries read the paged KV cache directly.  ``prefill_attention`` is the
+reference's dense entry (mini_engine/kernels/prefill.py:8-41, native op
+prefill.cu:15-98) for [batch, heads, tokens, head_dim] tensors.  Head dims
+that are multiples of 8 up to 256 run on bf16/fp16 MFMA tiles, other head
+sizes (up to 1024) on a generic HIP kernel.
 """
 
 from __future__ import annotations
@@ -88,3 +92,88 @@ def paged_prefill_attention(q, key_cache, value_cache, cu_seqlens_q, query_start
                  q.shape[1], kv_heads, head_dim, num_blocks, block_size, width, chunk_tokens,
                  ext.dtype_code(q.dtype), ws_ptr, ws_bytes, ext.current_stream(q.device))
     return output
+
+
+MAX_DENSE_CONTEXT = 1048576
+
+
+def _mfma_head_dim(head_dim):
+    return head_dim % 8 == 0 and head_dim <= 256
+
+
+def _dense_strides(tensor):
+    """(batch, head, token) strides in elements as the kernels read them:
+    dimensions of size 1 never move, so their stride is passed as 0."""
+    return tuple(st if size > 1 else 0 for size, st in zip(tensor.shape[:3], tensor.stride()[:3]))
+
+
+def _dense_layout_ok(tensor, head_dim):
+    """Innermost dim dense and, on the MFMA path, 16-byte rows: 16-byte
+    aligned base and strides in multiples of 8 elements."""
+    if head_dim > 1 and tensor.stride(3) != 1:
+        return False
+    if not _mfma_head_dim(head_dim):
+        return True
+    return tensor.data_ptr() % 16 == 0 and all(st % 8 == 0 for st in _dense_strides(tensor))
+
+
+def prefill_attention(q, k, v, backend="hip", *, query_start=0, out=None, workspace=None):
+    """Causal prefill attention over [batch, heads, tokens, head_dim] tensors.
+
+    Query row t of q attends keys [0, query_start + t] of k / v (GQA: query
+    head h reads kv head h // (q_heads // kv_heads)); the square case
+    (query_start 0, equal lengths) is plain causal attention.  Views are
+    read through their strides -- the transposes of [tokens, heads,
+    head_dim] tensors the model passes cost no copy -- and the result is
+    written token-major: without ``out`` the returned [batch, q_heads,
+    tokens, head_dim] tensor is a view of [batch, tokens, q_heads, head_dim]
+    storage, so the caller's transpose back to [tokens, heads, head_dim] is
+    contiguous.  ``out`` may supply any [batch, q_heads, tokens, head_dim]
+    tensor of q's dtype whose innermost dim is dense.
+    """
+    if backend != "hip":
+        raise ValueError("unknown prefill backend")
+    if (q.ndim != 4 or k.ndim != 4 or k.shape != v.shape or k.shape[1] == 0
+            or q.shape[1] % k.shape[1]):
+        raise ValueError("prefill expects [batch, heads, tokens, dim] and divisible GQA heads")
+    if (q.shape[0] != k.shape[0] or q.shape[-1] != k.shape[-1]
+            or q.dtype != k.dtype or q.dtype != v.dtype or q.device != k.device or q.device != v.device):
+        raise ValueError("prefill tensors must share batch, head_dim, dtype and device")
+    if (not isinstance(query_start, int) or isinstance(query_start, bool) or query_start < 0
+            or q.shape[-2] <= 0 or query_start + q.shape[-2] > k.shape[-2]):
+        raise ValueError("query_start and query length must fit the KV sequence")
+    if q.device.type != "cuda" or q.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("HIP prefill requires HIP FP16/BF16 tensors")
+    batch, q_heads, tokens, head_dim = q.shape
+    kv_heads, kv_tokens = k.shape[1], k.shape[2]
+    if head_dim > MAX_HEAD_DIM:
+        raise ValueError("HIP prefill supports head_dim up to 1024")
+    if query_start + tokens > MAX_DENSE_CONTEXT:
+        raise ValueError("HIP prefill supports at most 1048576 context tokens")
+    if not _dense_layout_ok(q, head_dim):
+        q = q.contiguous()
+    if k.stride() != v.stride() or not _dense_layout_ok(k, head_dim) or not _dense_layout_ok(v, head_dim):
+        k, v = k.contiguous(), v.contiguous()
+    if out is None:
+        result = torch.empty(batch, tokens, q_heads, head_dim, dtype=q.dtype, device=q.device).transpose(1, 2)
+    else:
+        if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+            raise ValueError("out must be a [batch, q_heads, tokens, head_dim] tensor of q's dtype and device")
+        if not _dense_layout_ok(out, head_dim):
+            raise ValueError("out must have a dense head_dim and 16-byte aligned rows")
+        result = out
+    if min(batch, q_heads, head_dim) == 0:
+        return result
+    lib = ext.load_hip_extension()
+    dtype = ext.dtype_code(q.dtype)
+    need = lib.dense_prefill_workspace_size(batch, tokens, q_heads, kv_heads, head_dim, query_start, dtype)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr() if workspace is not None else 0
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    with torch.cuda.device(q.device):
+        lib.call("mvme_prefill_attention", result.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                 batch, q_heads, kv_heads, tokens, kv_tokens, head_dim, query_start,
+                 *_dense_strides(q), *_dense_strides(k), *_dense_strides(result),
+                 dtype, ws_ptr, ws_bytes, ext.current_stream(q.device))
+    return result

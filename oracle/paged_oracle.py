@@ -202,6 +202,27 @@ def paged_prefill_attention(q, key_cache, value_cache, cu_seqlens_q, query_start
     return output
 
 
+def prefill_attention(q, k, v, *, query_start=0, cast=True):
+    """The torch dense prefill path (mini_engine/kernels/prefill.py:42-60).
+
+    q [B, Hq, T, D], k / v [B, Hkv, S, D]: K/V repeated over the GQA group
+    (repeat_interleave, :42-45), then SDPA -- with the bool mask
+    key <= query_start + t for a suffix (query_start > 0 or T != S, :46-53),
+    is_causal for the square case (:54-55).  Computed in fp32 (the reference
+    runs SDPA in the input dtype); cast=False keeps the fp32 result.
+    """
+    groups = q.shape[1] // k.shape[1]
+    key = k.repeat_interleave(groups, dim=1).float()
+    value = v.repeat_interleave(groups, dim=1).float()
+    query = q.float()
+    if query_start != 0 or q.shape[-2] != k.shape[-2]:
+        mask = torch.arange(k.shape[-2])[None, :] <= (query_start + torch.arange(q.shape[-2]))[:, None]
+        out = F.scaled_dot_product_attention(query, key, value, attn_mask=mask)
+    else:
+        out = F.scaled_dot_product_attention(query, key, value, is_causal=True)
+    return out.to(q.dtype) if cast else out
+
+
 def prefill_metadata(token_sequences, block_tables, query_starts, block_size):
     """Slot/position/offset rules of PrefillBatch (mini_engine/engine/batch.py:88-129).
 

@@ -30,7 +30,7 @@ def lib():
 
 def test_library_exports_every_declared_symbol(lib):
     symbols = declared_symbols()
-    assert len(symbols) == 16
+    assert len(symbols) == 18
     raw = ctypes.CDLL(str(hip_build.library_path()))
     for name in symbols:
         assert hasattr(raw, name), name
@@ -155,6 +155,45 @@ def test_scatter_and_prefill_reject_bad_arguments(lib):
                    None) == ext.OK
     assert _status(lib, "mvme_paged_prefill_attention", None, None, None, None, None, None, None, None, 0, 0, 16, 8,
                    128, 4, 16, 0, 0, 1, None, 0, None) == ext.OK
+
+
+def test_dense_prefill_plan_and_rejections(lib):
+    """mvme_prefill_attention (dense suffix prefill): its workspace plan and
+    argument checks, all before any launch (the pointers are never read)."""
+    bf16 = ext.BF16
+    # One 4096-token square prompt, Hq16/Hkv8/D128: 32 query blocks per kv
+    # head do not fill the CUs, so keys split into chunks of 512 (8 chunks).
+    rows = 4096 * 16
+    assert lib.dense_prefill_workspace_size(1, 4096, 16, 8, 128, 0, bf16) == \
+        8 * rows * 128 * 2 + 8 * rows * 2 * 4 + 4096 * 4
+    assert lib.dense_prefill_workspace_size(8, 4096, 16, 8, 128, 0, bf16) == 0  # enough blocks: no split
+    assert lib.dense_prefill_workspace_size(1, 4096, 16, 8, 20, 0, bf16) == 0  # generic kernel
+    assert lib.dense_prefill_workspace_size(1, 4096, 12, 8, 128, 0, bf16) == 0  # GQA mismatch
+    assert lib.dense_prefill_workspace_size(1, 64, 16, 8, 128, -1, bf16) == 0
+    assert lib.dense_prefill_workspace_size(1, 64, 16, 8, 128, 1 << 20, bf16) == 0  # context over 2^20
+    assert lib.dense_prefill_workspace_size(1, 64, 16, 8, 128, 0, 9) == 0
+
+    def call(batch=1, q_heads=16, kv_heads=8, tokens=64, kv_tokens=64, head_dim=128, start=0, ptr=256, out=256,
+             q_strides=None, kv_strides=None, dtype=bf16, workspace=None, workspace_bytes=0):
+        q_strides = q_strides or (q_heads * tokens * head_dim, tokens * head_dim, head_dim)
+        kv_strides = kv_strides or (kv_heads * kv_tokens * head_dim, kv_tokens * head_dim, head_dim)
+        return _status(lib, "mvme_prefill_attention", out, ptr, ptr, ptr, batch, q_heads, kv_heads, tokens, kv_tokens,
+                       head_dim, start, *q_strides, *kv_strides, *q_strides, dtype, workspace, workspace_bytes,
+                       None)
+
+    assert call(dtype=7) == ext.EINVAL and "FP16/BF16" in lib.last_error()
+    assert call(q_heads=12) == ext.EINVAL and "GQA" in lib.last_error()
+    assert call(head_dim=1032) == ext.EINVAL and "1024" in lib.last_error()
+    assert call(start=1) == ext.EINVAL and "query range exceeds KV sequence" in lib.last_error()
+    assert call(tokens=0) == ext.EINVAL and "query range" in lib.last_error()
+    assert call(ptr=None) == ext.EINVAL and "null pointer" in lib.last_error()
+    assert call(ptr=258) == ext.EINVAL and "16-byte aligned" in lib.last_error()
+    assert call(q_strides=(16 * 64 * 128, 64 * 128, 132)) == ext.EINVAL and "multiples of 8" in lib.last_error()
+    assert call(q_strides=(0, -8, 128)) == ext.EINVAL and "strides out of range" in lib.last_error()
+    assert call(kv_strides=(1 << 50, 64 * 128, 128), batch=4096) == ext.EINVAL and "out of range" in lib.last_error()
+    # A split plan without (or with too small) a workspace.
+    assert call(tokens=4096, kv_tokens=4096) == ext.EWORKSPACE and "workspace" in lib.last_error()
+    assert call(tokens=4096, kv_tokens=4096, workspace=256, workspace_bytes=1024) == ext.EWORKSPACE
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

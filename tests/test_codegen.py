@@ -68,7 +68,7 @@ def stray_waits(ins):
 
 def test_page_per_tile_kernels_do_not_wait_for_inflight_copies(prefill_asm):
     tile_kernels = [(n, ins) for n, ins in kernels(prefill_asm) if "ELi2E" in n]
-    assert len(tile_kernels) == 16  # fp16/bf16 x walk/no walk x tile shape 128/256 x full/zero-padded rows
+    assert len(tile_kernels) == 32  # fp16/bf16 x walk/no walk x tile shape 128/256 x full/zero-padded rows x paged/dense
     for name, ins in tile_kernels:
         assert sum(s.startswith("v_mfma") for s in ins) > 0, name
         assert stray_waits(ins) == [], name

@@ -13,7 +13,7 @@ from mini_engine_hip.cache.page_pool import PagePool
 from mini_engine_hip.engine.batch import PrefillBatch
 from mini_engine_hip.kernels.data import write_kv_cache, write_kv_cache_batch, write_kv_cache_slots
 from mini_engine_hip.kernels.paged import paged_attention
-from mini_engine_hip.kernels.prefill import paged_prefill_attention
+from mini_engine_hip.kernels.prefill import paged_prefill_attention, prefill_attention
 from oracle import paged_oracle
 
 
@@ -48,6 +48,37 @@ def test_cpu_tensors_are_refused_not_computed():
         write_kv_cache_slots(key, value, torch.tensor([3]), torch.ones(1, 2, 16).half(), torch.ones(1, 2, 16).half())
     with pytest.raises(ValueError, match="HIP paged prefill"):
         paged_prefill_attention(*inputs(), 4)
+
+
+def test_dense_prefill_contract_on_cpu():
+    """The reference's checks of prefill_attention (prefill.py:15-29) with its
+    messages, then the HIP requirements (prefill.py:35-40 for "cuda"); no
+    case reaches the library."""
+    gen = torch.Generator().manual_seed(71)
+    q = torch.randn(1, 4, 3, 16, generator=gen).half()
+    k = torch.randn(1, 2, 11, 16, generator=gen).half()
+    v = torch.randn(1, 2, 11, 16, generator=gen).half()
+    with pytest.raises(ValueError, match="unknown prefill backend"):
+        prefill_attention(q, k, v, "math", query_start=8)
+    with pytest.raises(ValueError, match="divisible GQA heads"):
+        prefill_attention(q[:, :3], k, v, query_start=8)
+    with pytest.raises(ValueError, match="divisible GQA heads"):
+        prefill_attention(q, k, v[:, :, :10], query_start=8)
+    with pytest.raises(ValueError, match="divisible GQA heads"):
+        prefill_attention(q[0], k, v, query_start=8)
+    with pytest.raises(ValueError, match="share batch, head_dim, dtype and device"):
+        prefill_attention(q, k.float(), v.float(), query_start=8)
+    with pytest.raises(ValueError, match="share batch, head_dim, dtype and device"):
+        prefill_attention(q[..., :8], k, v, query_start=8)
+    for start in (9, -1, True, 8.0):
+        with pytest.raises(ValueError, match="must fit the KV sequence"):
+            prefill_attention(q, k, v, query_start=start)
+    with pytest.raises(ValueError, match="must fit the KV sequence"):
+        prefill_attention(q[:, :, :0], k, v, query_start=8)
+    with pytest.raises(ValueError, match="HIP FP16/BF16"):
+        prefill_attention(q, k, v, query_start=8)
+    with pytest.raises(ValueError, match="HIP FP16/BF16"):
+        prefill_attention(q.float(), k.float(), v.float(), query_start=8)
 
 
 def test_slot_scatter_rejects_races_before_mutation():

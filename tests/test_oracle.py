@@ -223,6 +223,70 @@ def test_one_token_chunk_reduces_to_decode():
     torch.testing.assert_close(pre, dec, atol=1e-6, rtol=1e-5)
 
 
+def dense_as_paged(q, k, v, query_start, block, seed=0):
+    """The dense prefill's inputs laid out for the paged prefill: each batch
+    entry a sequence whose keys sit in shuffled pages of `block` tokens."""
+    batch, q_heads, tokens, dim = q.shape
+    kv_heads, kv_tokens = k.shape[1], k.shape[2]
+    context = query_start + tokens
+    width = -(-context // block)
+    pages = torch.randperm(batch * width + 3, generator=torch.Generator().manual_seed(seed))
+    kc = torch.zeros(batch * width + 3, block, kv_heads, dim, dtype=k.dtype)
+    vc = torch.zeros_like(kc)
+    tables = pages[:batch * width].view(batch, width).clone()
+    for b in range(batch):
+        for t in range(context):
+            kc[tables[b, t // block], t % block] = k[b, :, t]
+            vc[tables[b, t // block], t % block] = v[b, :, t]
+    packed = q.transpose(1, 2).reshape(batch * tokens, q_heads, dim)
+    meta = [torch.arange(0, batch * tokens + 1, tokens), torch.full((batch,), query_start),
+            tables, torch.full((batch,), context)]
+    return packed, kc, vc, meta
+
+
+def dense_case(seed, batch=2, q_heads=4, kv_heads=2, tokens=5, kv_tokens=13, dim=16):
+    gen = torch.Generator().manual_seed(seed)
+    return (torch.randn(batch, q_heads, tokens, dim, generator=gen),
+            torch.randn(batch, kv_heads, kv_tokens, dim, generator=gen),
+            torch.randn(batch, kv_heads, kv_tokens, dim, generator=gen))
+
+
+@pytest.mark.parametrize("query_start,tokens,kv_tokens", [(6, 5, 13), (8, 3, 11), (0, 9, 9), (0, 4, 10)])
+def test_dense_prefill_oracle_matches_paged_c_float64(query_start, tokens, kv_tokens):
+    """The dense path (prefill.py:42-60) equals the float64 C restatement of
+    the paged path on the same rows, laid into shuffled pages: mask start,
+    GQA mapping and the keys past query_start + T (never visible) agree."""
+    q, k, v = dense_case(query_start * 31 + tokens, tokens=tokens, kv_tokens=kv_tokens)
+    got = po.prefill_attention(q, k, v, query_start=query_start, cast=False)
+    packed, kc, vc, meta = dense_as_paged(q, k, v, query_start, 4)
+    want = c_oracle.paged_prefill(packed, kc, vc, *meta, 4)
+    got_packed = got.transpose(1, 2).reshape(packed.shape).double()
+    assert (got_packed - want).abs().max().item() <= 1e-5
+
+
+def test_dense_prefill_square_is_row_by_row_softmax():
+    """Brute force in float64: each query row's softmax over keys 0..t."""
+    q, k, v = dense_case(5, batch=1, q_heads=2, kv_heads=1, tokens=4, kv_tokens=4, dim=8)
+    got = po.prefill_attention(q, k, v, cast=False).double()
+    qd, kd, vd = q.double(), k.double(), v.double()
+    for h in range(2):
+        for t in range(4):
+            scores = [float(qd[0, h, t] @ kd[0, 0, j]) / math.sqrt(8) for j in range(t + 1)]
+            top = max(scores)
+            weights = [math.exp(x - top) for x in scores]
+            row = sum(w * vd[0, 0, j] for j, w in enumerate(weights)) / sum(weights)
+            assert (got[0, h, t] - row).abs().max().item() <= 1e-6
+
+
+def test_planted_dense_gqa_mistake_is_caught():
+    """Heads mapped by tiling (h % kv_heads) instead of h // group."""
+    q, k, v = dense_case(7, tokens=5, kv_tokens=13)
+    wrong = po.prefill_attention(q, k.repeat(1, 2, 1, 1), v.repeat(1, 2, 1, 1), query_start=6, cast=False)
+    packed, kc, vc, meta = dense_as_paged(q, k, v, 6, 4)
+    want = c_oracle.paged_prefill(packed, kc, vc, *meta, 4)
+    assert (wrong.transpose(1, 2).reshape(packed.shape).double() - want).abs().max().item() > 1e-3
+
+
 # ---------------------------------------------------------------------------
 # KV writes / gather (bit-exact)
 # ---------------------------------------------------------------------------
