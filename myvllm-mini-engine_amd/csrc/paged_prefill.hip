@@ -4,11 +4,13 @@
 // [cu[s], cu[s+1]), row i of s sits at absolute position starts[s] + i and
 // attends keys [0, starts[s] + i] of s through its block table.
 //
-// MFMA path (D = 128, G = Hq/Hkv dividing 256):
-//   Work item = (sequence, kv head, block of 256/G query tokens, chunk of
-//   `chunk` keys).  The 256 query rows of an item = (token, head-of-group)
-//   pairs that share every K/V tile; each of the 8 waves (two per SIMD) owns
-//   32 rows (two 16-row MFMA column blocks).  Long contexts with few query
+// MFMA path (D a multiple of 8 up to 256, any G = Hq/Hkv up to the tile's
+// rows; described for the D = 128 tile shape, PfShape below gives the 256 one):
+//   Work item = (sequence, kv head, block of floor(256/G) query tokens, chunk
+//   of `chunk` keys).  The 256 query rows of an item = (token, head-of-group)
+//   pairs that share every K/V tile (rows past tokens * G idle); each of the
+//   8 waves (two per SIMD) owns 32 rows (two 16-row MFMA column blocks).
+//   Head dims below the shape's are zero-padded in LDS.  Long contexts with few query
 //   blocks are cut into key chunks so that the work items spread over all
 //   CUs; items of a query block that needs several chunks write partials
 //   (the output normalised by its own probability sum -- bf16 for bf16
