@@ -390,6 +390,33 @@ struct PrefillLds {
     int incl[kWave];
 };
 
+// Item counts of the sequences held one per lane (lane s: sequence s), as
+// seq_items.  A lane walking a long sequence's query blocks one after the
+// other costs about 0.1 us per block (a dependent chain of integer and
+// reciprocal arithmetic); when some sequence has more than 8 blocks the wave
+// counts one sequence at a time instead, one block per lane, and sums
+// across the lanes.  The counts are the same either way.
+__device__ inline int wave_seq_items(const PrefillArgs& a, int chunk_len, const SeqMeta& m) {
+    const int lane = __lane_id();
+    const int64_t nb = m.n > 0 ? (m.n + a.qb - 1) / a.qb : 0;
+    if (a.max_chunks == 1 || __builtin_amdgcn_ballot_w64(nb > 8) == 0)
+        return seq_items(a, chunk_len, m.n, m.start, m.ctx);
+    int mine = 0;
+    const int held = min(a.num_seqs, kWave);
+    for (int s = 0; s < held; ++s) {
+        const int64_t n = lane_value(m.n, s);
+        if (n <= 0) continue;
+        const int64_t start = lane_value(m.start, s), ctx = lane_value(m.ctx, s);
+        const int64_t blocks = (n + a.qb - 1) / a.qb;
+        int part = 0;
+        for (int64_t b = lane; b < blocks; b += kWave)
+            part += chunks_of(chunk_len, block_kv_end(a, start, ctx, n, b * a.qb));
+        const int total = lane_value(wave_incl_scan(part), kWave - 1);
+        if (lane == s) mine = total;
+    }
+    return mine;
+}
+
 // The walk's index when every sequence fits one wave (num_seqs <= 64): lane
 // s keeps sequence s's metadata, item count and inclusive prefix of counts,
 // computed once per chunk length, so that a lookup is a ballot over the
@@ -399,7 +426,7 @@ struct PrefillLds {
 __device__ inline int walk_index(const PrefillArgs& a, int chunk_len, const SeqMeta& m, PrefillLds& lds,
                                 int& cnt, int& incl) {
     const int lane = __lane_id();
-    cnt = seq_items(a, chunk_len, m.n, m.start, m.ctx);
+    cnt = wave_seq_items(a, chunk_len, m);
     incl = wave_incl_scan(cnt);
     if (threadIdx.x < kWave) {
         lds.meta[lane] = m;
