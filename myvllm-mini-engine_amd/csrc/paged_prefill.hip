@@ -1022,13 +1022,15 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 // items with W work-groups:
 //   max(ceil(items / W) * (F + chunk / 64), (tiles + F * items) / W),
 // rounds of full items, never below the perfectly balanced total, with F
-// the fixed cost of an item (start-up and partial stores, about 2.5 tile
-// times), and all take the cheapest (ties: the smaller chunk).  Thread t
+// the fixed cost of an item in a walk (lookup, first page, Q and first-tile
+// latency, partial stores and the drained pipeline: about 5 tile times,
+// fitted to walks of one 2048- or 4096-token causal prompt timed at chunks
+// of 256 to 1024 keys), and all take the cheapest (ties: the smaller chunk).  Thread t
 // counts candidate t % 128 over every fourth query block (t / 128 picks
 // which), so the count costs a quarter of the blocks per thread; the sums
 // meet in the K ring, which the first copies fill only after the final
 // barrier here.
-constexpr float kItemFixedTiles = 2.5f;  // in 64-key tiles
+constexpr float kItemFixedTiles = 5.0f;  // in 64-key tiles
 constexpr int kChoiceCands = 128;
 constexpr int kChoiceSlices = kPfThreads / kChoiceCands;
 
