@@ -1046,7 +1046,24 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
     const int cand = a.chunk + KEYS * step * ci;
     const bool valid = cand <= cmax;  // candidate 0, the minimum, always is
     uint32_t items = 0, tiles = 0;
-    if (__builtin_amdgcn_ballot_w64(valid) != 0) {  // wave-uniform
+    // Up to 64 sequences the walk's index holds every sequence's metadata in
+    // LDS: each thread reads it there (independent broadcast reads) rather
+    // than by six dependent lane exchanges per sequence.
+    const bool indexed = a.num_seqs <= kWave;
+    if (indexed) __syncthreads();  // the index's LDS copy is complete
+    if (indexed && __builtin_amdgcn_ballot_w64(valid) != 0) {
+        int blk = 0;  // query blocks of the sequences before (uniform)
+        for (int j = 0; j < a.num_seqs; ++j) {
+            const SeqMeta mj = lds.meta[j];
+            const int nb = mj.n > 0 ? (int)ceil_div_u32((uint32_t)mj.n, (uint32_t)a.qb) : 0;
+            for (int k = ((slice - blk) % kChoiceSlices + kChoiceSlices) % kChoiceSlices; k < nb; k += kChoiceSlices) {
+                const uint32_t e = (uint32_t)block_kv_end(a, mj.start, mj.ctx, mj.n, (int64_t)k * a.qb);
+                items += e > 0 ? ceil_div_u32(e, (uint32_t)cand) : 1;
+                tiles += (e + KEYS - 1) / KEYS;
+            }
+            blk += nb;
+        }
+    } else if (!indexed && __builtin_amdgcn_ballot_w64(valid) != 0) {  // wave-uniform
         int blk = 0;  // query blocks of the sequences before (uniform)
         for (int s0 = 0; s0 < a.num_seqs; s0 += kWave) {
             // One sequence's metadata per lane, then every lane walks them all.
