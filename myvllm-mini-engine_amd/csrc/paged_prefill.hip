@@ -1025,14 +1025,21 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 // the fixed cost of an item in a walk (lookup, first page, Q and first-tile
 // latency, partial stores and the drained pipeline: about 5 tile times,
 // fitted to walks of one 2048- or 4096-token causal prompt timed at chunks
-// of 256 to 1024 keys), and all take the cheapest (ties: the smaller chunk).  Thread t
-// counts candidate t % 128 over every fourth query block (t / 128 picks
-// which), so the count costs a quarter of the blocks per thread; the sums
-// meet in the K ring, which the first copies fill only after the final
-// barrier here.
+// of 256 to 1024 keys), and all take the cheapest (ties: the smaller chunk).
+// Thread t counts candidate t % 128 over every fourth query block (t / 128
+// picks which), so the count costs a quarter of the blocks per thread; the
+// sums meet in the V ring, which the first copies fill only after the final
+// barrier here.  (The V ring, not the K ring: with heads narrower than the
+// tile the K ring's padded slots must stay zero, as they multiply the
+// queries' zero dims; the V ring's padded slots only reach output dims that
+// are never read.)
 constexpr float kItemFixedTiles = 5.0f;  // in 64-key tiles
 constexpr int kChoiceCands = 128;
 constexpr int kChoiceSlices = kPfThreads / kChoiceCands;
+constexpr int kChoiceListOffset = 1024;  // uint32 offset of the block-end list in the V ring (after the sums)
+constexpr int kChoiceMaxBlocks = 8192;   // blocks the list holds (32 KiB)
+static_assert((kChoiceListOffset + kChoiceMaxBlocks) * 4 <= kPfStages * kTileBytes, "list inside the V ring");
+static_assert(kChoiceSlices * kChoiceCands + kChoiceSlices <= kChoiceListOffset, "sums before the list");
 
 template <int KEYS, bool DENSE>
 __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta& first) {
@@ -1046,12 +1053,42 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
     const int cand = a.chunk + KEYS * step * ci;
     const bool valid = cand <= cmax;  // candidate 0, the minimum, always is
     uint32_t items = 0, tiles = 0;
-    // Up to 64 sequences the walk's index holds every sequence's metadata in
-    // LDS: each thread reads it there (independent broadcast reads) rather
-    // than by six dependent lane exchanges per sequence.
+    // Up to 64 sequences (lane j of every wave holds sequence j) the key
+    // ends of all query blocks go into one list in LDS first, each computed
+    // once, so that a thread's count is one read and one quotient per block;
+    // the list sits behind the sums' scratch in the V ring.  With more
+    // blocks than the list holds, each thread reads the walk index's
+    // metadata from LDS and computes the ends itself.
     const bool indexed = a.num_seqs <= kWave;
-    if (indexed) __syncthreads();  // the index's LDS copy is complete
-    if (indexed && __builtin_amdgcn_ballot_w64(valid) != 0) {
+    uint32_t* blk_end = reinterpret_cast<uint32_t*>(&lds.v[0][0]) + kChoiceListOffset;
+    int total_blocks = 0;
+    bool flat = false;
+    if (indexed) {
+        __syncthreads();  // the index's LDS copy is complete
+        const int nb = first.n > 0 ? (int)ceil_div_u32((uint32_t)first.n, (uint32_t)a.qb) : 0;
+        const int incl = wave_incl_scan(nb);
+        total_blocks = lane_value(incl, kWave - 1);
+        flat = total_blocks <= kChoiceMaxBlocks;
+        if (flat) {
+            for (int j = wave; j < a.num_seqs; j += kPfWaves) {
+                const int64_t n = lane_value(first.n, j), start = lane_value(first.start, j);
+                const int64_t ctx = lane_value(first.ctx, j);
+                const int nbj = lane_value(nb, j), off = lane_value(incl, j) - nbj;
+                for (int b = lane; b < nbj; b += kWave)
+                    blk_end[off + b] = (uint32_t)block_kv_end(a, start, ctx, n, (int64_t)b * a.qb);
+            }
+            __syncthreads();
+        }
+    }
+    if (flat) {
+        if (__builtin_amdgcn_ballot_w64(valid) != 0) {  // wave-uniform
+            for (int b = slice; b < total_blocks; b += kChoiceSlices) {
+                const uint32_t e = blk_end[b];
+                items += e > 0 ? ceil_div_u32(e, (uint32_t)cand) : 1;
+                tiles += (e + KEYS - 1) / KEYS;
+            }
+        }
+    } else if (indexed && __builtin_amdgcn_ballot_w64(valid) != 0) {
         int blk = 0;  // query blocks of the sequences before (uniform)
         for (int j = 0; j < a.num_seqs; ++j) {
             const SeqMeta mj = lds.meta[j];
@@ -1083,7 +1120,7 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
             }
         }
     }
-    uint32_t* sc_items = reinterpret_cast<uint32_t*>(&lds.k[0][0]);  // [slice][candidate]
+    uint32_t* sc_items = reinterpret_cast<uint32_t*>(&lds.v[0][0]);  // [slice][candidate]
     uint32_t* sc_tiles = sc_items + kChoiceSlices * kChoiceCands;     // [slice]
     sc_items[slice * kChoiceCands + ci] = items;
     if (ci == 0) sc_tiles[slice] = tiles;
