@@ -360,6 +360,19 @@ __device__ inline void lds_dma16_s(const uint8_t* sbase, uint32_t voff, uint32_t
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(voff), "s"(gu), "s"(base) : "m0");
 }
 
+// Minimum over the 64 lanes of a wave, returned to every lane: each 16-lane
+// row's minimum by DPP (quad swaps, then the half-row and row mirrors), then
+// the four rows' by readlane.
+__device__ inline uint32_t wave_min_u32(uint32_t x) {
+    x = min(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppQuadSwap1, 0xf, 0xf, false));
+    x = min(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppQuadSwap2, 0xf, 0xf, false));
+    x = min(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowHalfMirror, 0xf, 0xf, false));
+    x = min(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, kDppRowMirror, 0xf, 0xf, false));
+    const uint32_t lo = min((uint32_t)lane_value((int)x, 0), (uint32_t)lane_value((int)x, 16));
+    const uint32_t hi = min((uint32_t)lane_value((int)x, 32), (uint32_t)lane_value((int)x, 48));
+    return min(lo, hi);
+}
+
 constexpr int kPagesPerLane = 0;
 constexpr int kPagesPerRows = 1;
 constexpr int kPagesPerTile = 2;
@@ -1125,33 +1138,34 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
     sc_items[slice * kChoiceCands + ci] = items;
     if (ci == 0) sc_tiles[slice] = tiles;
     __syncthreads();
-    uint64_t key = ~0ull;
-    if (slice == 0 && valid) {
-        uint32_t it_sum = 0, tl_sum = 0;
+    // Slice 0 (threads 0..127: candidate ci = thread, waves 0 and 1) prices
+    // the candidates; each of those waves takes its cheapest (the lowest lane
+    // among equal costs: the smaller chunk).  Non-negative floats order like
+    // their bit patterns; a candidate past the capacity costs all ones.
+    static_assert(kChoiceCands == 2 * kWave, "slice 0 is waves 0 and 1");
+    if (wave < 2) {
+        uint32_t cost_bits = 0xffffffffu;
+        if (valid) {
+            uint32_t it_sum = 0, tl_sum = 0;
 #pragma unroll
-        for (int k = 0; k < kChoiceSlices; ++k) {
-            it_sum += sc_items[k * kChoiceCands + ci];
-            tl_sum += sc_tiles[k];
+            for (int k = 0; k < kChoiceSlices; ++k) {
+                it_sum += sc_items[k * kChoiceCands + ci];
+                tl_sum += sc_tiles[k];
+            }
+            const uint32_t w = (uint32_t)a.item_stride;
+            const float rounds = (float)((it_sum + w - 1) / w);
+            const float cost = fmaxf(rounds * (kFixed + (float)(cand / KEYS)),
+                                     ((float)tl_sum + kFixed * (float)it_sum) / (float)w);
+            cost_bits = __float_as_uint(cost);
         }
-        const uint32_t w = (uint32_t)a.item_stride;
-        const float rounds = (float)((it_sum + w - 1) / w);
-        const float cost = fmaxf(rounds * (kFixed + (float)(cand / KEYS)),
-                                 ((float)tl_sum + kFixed * (float)it_sum) / (float)w);
-        // Non-negative floats order like their bit patterns.
-        key = ((uint64_t)__float_as_uint(cost) << 32) | (uint32_t)ci;
+        const uint32_t least = wave_min_u32(cost_bits);
+        const uint64_t hit = __builtin_amdgcn_ballot_w64(cost_bits == least);
+        if (lane == 0) lds.pick[wave] = ((uint64_t)least << 32) | (uint32_t)(wave * kWave + __builtin_ctzll(hit));
     }
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const uint64_t o = ((uint64_t)(uint32_t)__shfl_xor((int)(key >> 32), off) << 32) |
-                           (uint32_t)__shfl_xor((int)(uint32_t)key, off);
-        key = o < key ? o : key;
-    }
-    if (lane == 0) lds.pick[wave] = key;
+    // The sums and the block list (V ring) are read before this barrier, so
+    // the copies that follow may overwrite them; the picks are not in a ring.
     __syncthreads();
-    uint64_t best = lds.pick[0];
-#pragma unroll
-    for (int w = 1; w < kPfWaves; ++w) best = lds.pick[w] < best ? lds.pick[w] : best;
-    __syncthreads();  // every thread has read the sums and picks before the ring is refilled
+    const uint64_t best = lds.pick[0] < lds.pick[1] ? lds.pick[0] : lds.pick[1];
     return a.chunk + KEYS * step * (int)(uint32_t)best;
 }
 
