@@ -126,3 +126,33 @@ def test_caller_output_and_workspace_match_the_default():
     assert got is out and out.is_contiguous()
     assert torch.equal(out, want)
     check(out, q, k, v, 2900, dtype)
+
+
+def test_sliced_views_differing_kv_strides_and_graph_replay():
+    """Queries sliced out of a longer token range (a batch stride that is not
+    a multiple of the tensor's own size), K and V with different layouts
+    (the wrapper then copies both), and the call captured in a HIP graph and
+    replayed with new query values."""
+    dtype = torch.float16
+    gen = torch.Generator().manual_seed(12)
+    big_q = randn(gen, 2, 8, 300, 64, dtype=dtype)
+    q = big_q[:, :, 40:140]                                   # [2, 8, 100, 64], token window of a longer range
+    k = randn(gen, 2, 4, 400, 64, dtype=dtype)
+    v = randn(gen, 2, 400, 4, 64, dtype=dtype).transpose(1, 2)  # same shape as k, other strides
+    assert k.stride() != v.stride()
+    print("dense prefill sliced views / differing strides", flush=True)
+    out = prefill_attention(q, k, v, "hip", query_start=250)
+    torch.cuda.synchronize()
+    check(out, q, k, v, 250, dtype)
+    static_out = torch.empty_like(q)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        prefill_attention(q, k, v, "hip", query_start=250, out=static_out)
+    for step in range(3):
+        big_q.copy_(randn(gen, 2, 8, 300, 64, dtype=dtype))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = prefill_attention(q, k, v, "hip", query_start=250)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, eager), step
+        check(static_out, q, k, v, 250, dtype)
