@@ -175,6 +175,13 @@ __device__ inline uint32_t ceil_div_u32(uint32_t e, uint32_t d) {
     return q;
 }
 
+// Query blocks of a sequence with n packed queries (n < 2^31: offsets are
+// clamped to the packed rows), by the float-corrected quotient rather than a
+// 64-bit division (a long instruction sequence on the lookup's critical path).
+__device__ inline int query_blocks(const PrefillArgs& a, int64_t n) {
+    return n > 0 ? (int)ceil_div_u32((uint32_t)n, (uint32_t)a.qb) : 0;
+}
+
 // kv_end <= table capacity < 2^31, so 32-bit unsigned arithmetic is exact.
 __device__ inline int chunks_of(int chunk_len, int64_t kv_end) {
     return kv_end > 0 ? (int)ceil_div_u32((uint32_t)kv_end, (uint32_t)chunk_len) : 1;
@@ -185,7 +192,7 @@ __device__ inline int chunks_of(int chunk_len, int64_t kv_end) {
 // Without key splitting every block is exactly one item.
 __device__ inline int seq_items(const PrefillArgs& a, int chunk_len, int64_t n, int64_t start, int64_t ctx) {
     if (n <= 0) return 0;
-    if (a.max_chunks == 1) return (int)((n + a.qb - 1) / a.qb);
+    if (a.max_chunks == 1) return query_blocks(a, n);
     int count = 0;
     for (int64_t b0 = 0; b0 < n; b0 += a.qb) count += chunks_of(chunk_len, block_kv_end(a, start, ctx, n, b0));
     return count;
@@ -258,7 +265,7 @@ __device__ inline bool find_item(const PrefillArgs& a, int chunk_len, int item, 
             it.ctx = lane_value(ctx, sel);
             // Query blocks from the last (longest key range) to the first, so
             // that the work-groups dispatched last are the short ones.
-            const int64_t nblocks = (it.qlen + a.qb - 1) / a.qb;
+            const int64_t nblocks = query_blocks(a, it.qlen);
             it.chunk_len = chunk_len;
             if (a.max_chunks == 1) {  // one item per block: no search
                 const int64_t b0 = (nblocks - 1 - rem) * a.qb;
@@ -411,7 +418,7 @@ struct PrefillLds {
 // across the lanes.  The counts are the same either way.
 __device__ inline int wave_seq_items(const PrefillArgs& a, int chunk_len, const SeqMeta& m) {
     const int lane = __lane_id();
-    const int64_t nb = m.n > 0 ? (m.n + a.qb - 1) / a.qb : 0;
+    const int64_t nb = query_blocks(a, m.n);
     if (a.max_chunks == 1 || __builtin_amdgcn_ballot_w64(nb > 8) == 0)
         return seq_items(a, chunk_len, m.n, m.start, m.ctx);
     int mine = 0;
@@ -420,7 +427,7 @@ __device__ inline int wave_seq_items(const PrefillArgs& a, int chunk_len, const 
         const int64_t n = lane_value(m.n, s);
         if (n <= 0) continue;
         const int64_t start = lane_value(m.start, s), ctx = lane_value(m.ctx, s);
-        const int64_t blocks = (n + a.qb - 1) / a.qb;
+        const int64_t blocks = query_blocks(a, n);
         int part = 0;
         for (int64_t b = lane; b < blocks; b += kWave)
             part += chunks_of(chunk_len, block_kv_end(a, start, ctx, n, b * a.qb));
@@ -465,7 +472,7 @@ __device__ inline bool find_item_lanes(const PrefillArgs& a, int chunk_len, int 
     it.chunk_len = chunk_len;
     // Query blocks from the last to the first (as find_item), 64 at a time:
     // lane l takes the l-th block of the group.
-    const int64_t nblocks = (it.qlen + a.qb - 1) / a.qb;
+    const int64_t nblocks = query_blocks(a, it.qlen);
     for (int64_t g0 = 0; g0 < nblocks; g0 += kWave) {
         const int64_t bi = nblocks - 1 - (g0 + lane);
         int64_t e = 0;
@@ -1122,7 +1129,7 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
             const int cnt = min(kWave, a.num_seqs - s0);
             for (int j = 0; j < cnt; ++j) {
                 const int64_t nj = __shfl(n, j), sj = __shfl(start, j), cj = __shfl(ctx, j);
-                const int nb = nj > 0 ? (int)((nj + a.qb - 1) / a.qb) : 0;
+                const int nb = query_blocks(a, nj);
                 for (int k = ((slice - blk) % kChoiceSlices + kChoiceSlices) % kChoiceSlices; k < nb;
                      k += kChoiceSlices) {
                     const uint32_t e = (uint32_t)block_kv_end(a, sj, cj, nj, (int64_t)k * a.qb);
