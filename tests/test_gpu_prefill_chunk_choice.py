@@ -1,0 +1,115 @@
+"""The paged prefill walk's chunk choice on the device (choose_chunk in
+paged_prefill.hip).
+
+Every chunk length gives a correct result, so the outputs alone cannot show
+which chunk the device took.  Two checks pin it:
+
+* the chunk count that the first item of each query block records for every
+  token of the block (an int per packed token, the workspace's last region)
+  equals the count of the chunk that a host restatement of the cost model
+  picks;
+* the call gives the same bits as a call given that chunk explicitly.
+
+The model (restated from the kernel): candidates are the host's chunk
+max(512, capacity/32 rounded up to 64 keys) plus multiples of 64*step keys,
+128 of them up to the capacity; each costs
+max(ceil(items/W) * (5 + chunk/64), (tiles + 5 * items) / W) in fp32 with
+W = 256 / kv_heads work-groups per kv head; the cheapest wins, ties going to
+the smaller chunk.  The choice is made only when the host's chunk gives more
+than one round of items.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from mini_engine_hip import workloads
+from mini_engine_hip.kernels import hip_extension as ext
+from mini_engine_hip.kernels.prefill import paged_prefill_attention
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+CUS = 256
+KEYS = 64
+FIXED = np.float32(5.0)
+NAMES = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+PRIORS8 = [2220, 601, 877, 1126, 1381, 3550, 2532, 347]
+
+
+def ceil_div(a, b):
+    return -(-a // b)
+
+
+def block_ends(priors, new_tokens, qb, cap):
+    return [min(p + min(q0 + qb, new_tokens), cap) for p in priors for q0 in range(0, new_tokens, qb)]
+
+
+def model_chunk(priors, new_tokens, block_size, table_width, q_heads, kv_heads):
+    qb = 256 // (q_heads // kv_heads)
+    cap = table_width * block_size
+    host = max(512, ceil_div(ceil_div(cap, 32), KEYS) * KEYS)
+    cmax = ceil_div(cap, KEYS) * KEYS
+    step = max(1, ceil_div((cmax - host) // KEYS, 128))
+    ends = block_ends(priors, new_tokens, qb, cap)
+    w = max(1, CUS // kv_heads)
+
+    def items(c):
+        return sum(ceil_div(e, c) if e > 0 else 1 for e in ends)
+
+    if items(host) <= w:
+        return host, False
+    tiles = sum(ceil_div(e, KEYS) for e in ends)
+    best = None
+    for i in range(128):
+        c = host + KEYS * step * i
+        if c > cmax:
+            break
+        n = items(c)
+        rounds = np.float32(ceil_div(n, w))
+        cost = max(rounds * (FIXED + np.float32(c // KEYS)),
+                   (np.float32(tiles) + FIXED * np.float32(n)) / np.float32(w))
+        if best is None or cost < best[0]:
+            best = (cost, c)
+    return best[1], True
+
+
+@pytest.mark.parametrize("num_seqs,new_tokens,priors", [
+    (1, 2048, [0]),
+    (1, 4096, [0]),          # 832 and 1408 tie in the model: the smaller wins
+    (2, 2048, [0, 1000]),
+    (8, 512, PRIORS8),
+    (16, 256, None),
+    (1, 512, [16000]),       # capacity 16,640: candidates step by 128 keys
+    (4, 128, [8000, 12000, 3000, 30000]),
+])
+def test_device_choice_matches_the_model(num_seqs, new_tokens, priors):
+    c = workloads.chunked_prefill_case(device=torch.device(DEV), num_seqs=num_seqs, new_tokens=new_tokens,
+                                       priors=priors)
+    args = [c[n] for n in NAMES]
+    q, kc = c["q"], c["key_cache"]
+    priors = c["priors"]
+    tokens, q_heads = q.shape[0], q.shape[1]
+    _, block_size, kv_heads, head_dim = kc.shape
+    width = c["block_tables"].shape[1]
+    want, chose = model_chunk(priors, new_tokens, block_size, width, q_heads, kv_heads)
+    print(f"chunk choice {num_seqs}x{new_tokens}: model {want} (choice made: {chose})", flush=True)
+    assert chose, "shape must need more than one round of items at the host's chunk"
+
+    lib = ext.load_hip_extension()
+    need = lib.prefill_workspace_size(num_seqs, tokens, q_heads, kv_heads, head_dim, block_size, width, 0,
+                                      ext.dtype_code(q.dtype))
+    workspace = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    auto = paged_prefill_attention(*args, block_size, backend="hip", validate=False, workspace=workspace)
+    explicit = paged_prefill_attention(*args, block_size, backend="hip", validate=False, chunk_tokens=want)
+    torch.cuda.synchronize()
+
+    tok_bytes = (tokens * 4 + 15) // 16 * 16
+    counts = workspace[need - tok_bytes:need - tok_bytes + tokens * 4].cpu().view(torch.int32).tolist()
+    qb = 256 // (q_heads // kv_heads)
+    expected = []
+    for p in priors:
+        for t in range(new_tokens):
+            end = min(p + min(t // qb * qb + qb, new_tokens), width * block_size)
+            expected.append(ceil_div(end, want))
+    assert counts == expected
+    assert torch.equal(auto, explicit)
