@@ -1036,10 +1036,11 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 // Chunk choice for a walk (the caller's chunk is the smallest allowed: it
 // bounds the workspace).  The best chunk puts the item count just under a
 // multiple of the walkers, and which chunk that is depends on the lengths,
-// which only the device sees.  Every work-group evaluates the same 128
-// candidates a.chunk + 64*step*c (c < 128, up to the capacity) against the
-// same estimate of the makespan (in tile times) of walking one kv head's
-// items with W work-groups:
+// which only the device sees.  Every work-group evaluates the same
+// candidates a.chunk + 64*step*c (c < 128, or c < 512 when there are fewer
+// than 16 query blocks; up to the capacity) against the same estimate of
+// the makespan (in tile times) of walking one kv head's items with W
+// work-groups:
 //   max(ceil(items / W) * (F + chunk / 64), (tiles + F * items) / W),
 // rounds of full items, never below the perfectly balanced total, with F
 // the fixed cost of an item in a walk (lookup, first page, Q and first-tile
@@ -1047,15 +1048,18 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 // fitted to walks of one 2048- or 4096-token causal prompt timed at chunks
 // of 256 to 1024 keys), and all take the cheapest (ties: the smaller chunk).
 // Thread t counts candidate t % 128 over every fourth query block (t / 128
-// picks which), so the count costs a quarter of the blocks per thread; the
-// sums meet in the V ring, which the first copies fill only after the final
-// barrier here.  (The V ring, not the K ring: with heads narrower than the
+// picks which), so the count costs a quarter of the blocks per thread; with
+// fewer than 16 blocks (a few long requests: large capacities, so a coarse
+// step) thread t counts candidate t over all of them, which puts the
+// candidates 4 times closer.  The sums meet in the V ring, which the first
+// copies fill only after the final barrier here.  (The V ring, not the K ring: with heads narrower than the
 // tile the K ring's padded slots must stay zero, as they multiply the
 // queries' zero dims; the V ring's padded slots only reach output dims that
 // are never read.)
 constexpr float kItemFixedTiles = 5.0f;  // in 64-key tiles
 constexpr int kChoiceCands = 128;
 constexpr int kChoiceSlices = kPfThreads / kChoiceCands;
+constexpr int kChoiceWideBlocks = 16;    // below this many blocks: one candidate per thread
 constexpr int kChoiceListOffset = 1024;  // uint32 offset of the block-end list in the V ring (after the sums)
 constexpr int kChoiceMaxBlocks = 8192;   // blocks the list holds (32 KiB)
 static_assert((kChoiceListOffset + kChoiceMaxBlocks) * 4 <= kPfStages * kTileBytes, "list inside the V ring");
@@ -1065,13 +1069,9 @@ template <int KEYS, bool DENSE>
 __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta& first) {
     constexpr float kFixed = kItemFixedTiles * 64.f / KEYS;  // an item's fixed cost in tiles of KEYS keys
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int ci = tid % kChoiceCands, slice = tid / kChoiceCands;
     const int cap = a.table_width * a.block_size;
     const int cmax = (cap + KEYS - 1) / KEYS * KEYS;
     const int span = (cmax - a.chunk) / KEYS;  // candidate steps above the minimum
-    const int step = max(1, (span + kChoiceCands - 1) / kChoiceCands);
-    const int cand = a.chunk + KEYS * step * ci;
-    const bool valid = cand <= cmax;  // candidate 0, the minimum, always is
     uint32_t items = 0, tiles = 0;
     // Up to 64 sequences (lane j of every wave holds sequence j) the key
     // ends of all query blocks go into one list in LDS first, each computed
@@ -1100,9 +1100,18 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
             __syncthreads();
         }
     }
+    // Uniform over the work-group: every wave derives total_blocks from the
+    // same metadata.
+    const bool wide = flat && total_blocks < kChoiceWideBlocks;
+    const int cands = wide ? kPfThreads : kChoiceCands;
+    const int slices = wide ? 1 : kChoiceSlices;
+    const int ci = tid % cands, slice = tid / cands;
+    const int step = max(1, (span + cands - 1) / cands);
+    const int cand = a.chunk + KEYS * step * ci;
+    const bool valid = cand <= cmax;  // candidate 0, the minimum, always is
     if (flat) {
         if (__builtin_amdgcn_ballot_w64(valid) != 0) {  // wave-uniform
-            for (int b = slice; b < total_blocks; b += kChoiceSlices) {
+            for (int b = slice; b < total_blocks; b += slices) {
                 const uint32_t e = blk_end[b];
                 items += e > 0 ? ceil_div_u32(e, (uint32_t)cand) : 1;
                 tiles += (e + KEYS - 1) / KEYS;
@@ -1141,22 +1150,26 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
         }
     }
     uint32_t* sc_items = reinterpret_cast<uint32_t*>(&lds.v[0][0]);  // [slice][candidate]
-    uint32_t* sc_tiles = sc_items + kChoiceSlices * kChoiceCands;     // [slice]
-    sc_items[slice * kChoiceCands + ci] = items;
+    uint32_t* sc_tiles = sc_items + kPfThreads;                       // [slice]
+    sc_items[slice * cands + ci] = items;
     if (ci == 0) sc_tiles[slice] = tiles;
     __syncthreads();
-    // Slice 0 (threads 0..127: candidate ci = thread, waves 0 and 1) prices
-    // the candidates; each of those waves takes its cheapest (the lowest lane
-    // among equal costs: the smaller chunk).  Non-negative floats order like
-    // their bit patterns; a candidate past the capacity costs all ones.
+    // Slice 0 (candidate ci = thread: waves 0 and 1, or every wave when
+    // wide) prices the candidates; each of those waves takes its cheapest
+    // (the lowest lane among equal costs: the smaller chunk).  Non-negative
+    // floats order like their bit patterns; a candidate past the capacity
+    // costs all ones.
     static_assert(kChoiceCands == 2 * kWave, "slice 0 is waves 0 and 1");
-    if (wave < 2) {
+    static_assert(kChoiceSlices * kChoiceCands == kPfThreads, "one candidate slot per thread");
+    const int pricing_waves = wide ? kPfWaves : 2;
+    if (wave < pricing_waves) {
         uint32_t cost_bits = 0xffffffffu;
         if (valid) {
             uint32_t it_sum = 0, tl_sum = 0;
 #pragma unroll
             for (int k = 0; k < kChoiceSlices; ++k) {
-                it_sum += sc_items[k * kChoiceCands + ci];
+                if (k >= slices) break;
+                it_sum += sc_items[k * cands + ci];
                 tl_sum += sc_tiles[k];
             }
             const uint32_t w = (uint32_t)a.item_stride;
@@ -1172,7 +1185,8 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
     // The sums and the block list (V ring) are read before this barrier, so
     // the copies that follow may overwrite them; the picks are not in a ring.
     __syncthreads();
-    const uint64_t best = lds.pick[0] < lds.pick[1] ? lds.pick[0] : lds.pick[1];
+    uint64_t best = lds.pick[0];
+    for (int w = 1; w < pricing_waves; ++w) best = lds.pick[w] < best ? lds.pick[w] : best;
     return a.chunk + KEYS * step * (int)(uint32_t)best;
 }
 

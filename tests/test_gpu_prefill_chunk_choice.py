@@ -12,7 +12,8 @@ which chunk the device took.  Two checks pin it:
 
 The model (restated from the kernel): candidates are the host's chunk
 max(512, capacity/32 rounded up to 64 keys) plus multiples of 64*step keys,
-128 of them up to the capacity; each costs
+128 of them (512 with fewer than 16 query blocks) up to the capacity; each
+costs
 max(ceil(items/W) * (5 + chunk/64), (tiles + 5 * items) / W) in fp32 with
 W = 256 / kv_heads work-groups per kv head; the cheapest wins, ties going to
 the smaller chunk.  The choice is made only when the host's chunk gives more
@@ -49,8 +50,9 @@ def model_chunk(priors, new_tokens, block_size, table_width, q_heads, kv_heads):
     cap = table_width * block_size
     host = max(512, ceil_div(ceil_div(cap, 32), KEYS) * KEYS)
     cmax = ceil_div(cap, KEYS) * KEYS
-    step = max(1, ceil_div((cmax - host) // KEYS, 128))
     ends = block_ends(priors, new_tokens, qb, cap)
+    cands = 512 if len(priors) <= 64 and len(ends) < 16 else 128
+    step = max(1, ceil_div((cmax - host) // KEYS, cands))
     w = max(1, CUS // kv_heads)
 
     def items(c):
@@ -60,7 +62,7 @@ def model_chunk(priors, new_tokens, block_size, table_width, q_heads, kv_heads):
         return host, False
     tiles = sum(ceil_div(e, KEYS) for e in ends)
     best = None
-    for i in range(128):
+    for i in range(cands):
         c = host + KEYS * step * i
         if c > cmax:
             break
@@ -79,8 +81,9 @@ def model_chunk(priors, new_tokens, block_size, table_width, q_heads, kv_heads):
     (2, 2048, [0, 1000]),
     (8, 512, PRIORS8),
     (16, 256, None),
-    (1, 512, [16000]),       # capacity 16,640: candidates step by 128 keys
-    (4, 128, [8000, 12000, 3000, 30000]),
+    (1, 512, [16000]),       # 4 blocks: 512 candidates, one per 64 keys
+    (4, 128, [8000, 12000, 3000, 30000]),  # 512 candidates take 1792 (128 would step by 256 keys: 1984)
+    (2, 1024, [20000, 40000]),  # 16 blocks: 128 candidates stepping by 320 keys
 ])
 def test_device_choice_matches_the_model(num_seqs, new_tokens, priors):
     c = workloads.chunked_prefill_case(device=torch.device(DEV), num_seqs=num_seqs, new_tokens=new_tokens,
