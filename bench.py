@@ -20,7 +20,7 @@ The CPU leg (field "cpu_baseline", off with --no-cpu-baseline) is the only
 part that touches the oracle: it times the reference's torch path (restated
 in the oracle) on this host on bounded samples -- one headline decode
 layer, and the chunked-prefill workload's KV scatter and prefill attention
--- and, as the checker, computes the reference outputs that every GPU
+-- and computes the reference outputs that every GPU
 result above is compared with (the error fields are null without it).
 
 Prints ONE JSON line.
@@ -297,7 +297,7 @@ def _median_seconds(fn, budget_s, min_runs=5, max_runs=20):
 class CpuLeg:
     """The CPU leg: the reference's torch path restated in the oracle, on the
     host cores.  It is the only user of the oracle in this file -- as the
-    timed CPU baseline and as the checker that computes the reference outputs
+    timed CPU baseline and to compute the reference outputs
     the GPU results are compared with."""
 
     def __init__(self, torch):
@@ -306,7 +306,7 @@ class CpuLeg:
         self.torch = torch
         self.oracle = paged_oracle
 
-    # Reference outputs (the checker).
+    # Reference outputs (the oracle).
     def decode(self, tensors, block_size):
         return self.oracle.fp32_oracle(tensors, block_size)
 

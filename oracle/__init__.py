@@ -1,6 +1,6 @@
 """CPU oracle of the paged-attention hot path -- TEST INFRASTRUCTURE ONLY.
 
-Imported only by tests/, __graft_entry__.smoke() (as the checker) and
+Imported only by tests/, __graft_entry__.smoke() (for the reference outputs) and
 bench.py's cpu_baseline leg (as the timed CPU path).  The HIP product path in
 myvllm-mini-engine_amd/ never imports it.
 

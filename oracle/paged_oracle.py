@@ -1,7 +1,8 @@
 """CPU oracle of the paged-attention hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this module, and only as the checker or the timed CPU baseline.  The
+import this module, and only to compute the outputs GPU results are
+compared with, or as the timed CPU baseline.  The
 HIP product path never calls it.
 
 Every function restates, in this repository's own code, one CPU algorithm of

@@ -4,7 +4,7 @@ Reads the reference's own benchmark record
 reports/data/engine_comparison_20261026.json (cases B1/ctx128, B8/ctx512,
 B32/ctx2048; seed 20261026, fp16, block 256) and writes the input-tensor
 hashes to tests/golden/make_case_manifest.json.  Run in the container that
-has the reference checkout; the GPU box never runs this.
+has the reference checkout; no GPU run uses this script.
 """
 
 import json
