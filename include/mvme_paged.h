@@ -264,7 +264,9 @@ size_t mvme_prefill_attention_workspace_size(int64_t batch, int64_t q_tokens, in
  * the transposes of [tokens, heads, head_dim] tensors need no copy.  For
  * head dims that are multiples of 8 up to 256 (the MFMA path) every pointer
  * must be 16-byte aligned and every stride a multiple of 8 elements; other
- * head dims (up to 1024) need 2-byte alignment.  workspace: at least
+ * head dims (up to 1024) need 2-byte alignment.  The output's elements must
+ * be distinct (no stride 0 over more than one element, no interleaved
+ * dimensions); inputs may overlap.  workspace: at least
  * mvme_prefill_attention_workspace_size(...) bytes (may be NULL when 0).
  * Runs the paged prefill kernels with each batch entry as one sequence whose
  * keys are a single page.

@@ -1789,6 +1789,27 @@ bool strided_span_ok(int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t n2,
     return span < ((__int128)1 << 60);
 }
 
+// No two elements of a [n0, n1, n2, d] view (innermost stride 1, strides
+// non-negative) share an address: taken by increasing stride, every
+// dimension of more than one element steps past all the offsets the smaller
+// ones reach.  (Holds for every layout torch makes without expand().)
+bool view_disjoint(int64_t n0, int64_t s0, int64_t n1, int64_t s1, int64_t n2, int64_t s2, int64_t d) {
+    int64_t n[3] = {n0, n1, n2}, s[3] = {s0, s1, s2};
+    for (int i = 0; i < 3; ++i)
+        for (int j = i + 1; j < 3; ++j)
+            if (s[j] < s[i]) {
+                std::swap(n[i], n[j]);
+                std::swap(s[i], s[j]);
+            }
+    __int128 reach = d;  // offsets [0, reach) are taken
+    for (int i = 0; i < 3; ++i) {
+        if (n[i] <= 1) continue;
+        if ((__int128)s[i] < reach) return false;
+        reach += (__int128)s[i] * (n[i] - 1);
+    }
+    return true;
+}
+
 }  // namespace
 
 extern "C" size_t mvme_prefill_attention_workspace_size(int64_t batch, int64_t q_tokens, int64_t q_heads,
@@ -1823,6 +1844,8 @@ extern "C" int mvme_prefill_attention(void* out, const void* q, const void* key,
         !strided_span_ok(batch, out_batch_stride, q_heads, out_head_stride, q_tokens, out_token_stride, head_dim) ||
         !strided_span_ok(batch, kv_batch_stride, kv_heads, kv_head_stride, kv_tokens, kv_token_stride, head_dim))
         return fail(MVME_EINVAL, "prefill strides out of range");
+    if (!view_disjoint(batch, out_batch_stride, q_heads, out_head_stride, q_tokens, out_token_stride, head_dim))
+        return fail(MVME_EINVAL, "prefill output rows overlap");
     const int64_t ctx = query_start + q_tokens;
     const int64_t bs = dense_block(ctx);
     const int64_t rows = batch * q_tokens;

@@ -117,6 +117,23 @@ def _dense_layout_ok(tensor, head_dim):
     return tensor.data_ptr() % 16 == 0 and all(st % 8 == 0 for st in _dense_strides(tensor))
 
 
+def _dense_disjoint(tensor):
+    """No two elements of a [batch, heads, tokens, head_dim] tensor share an
+    address: taken by increasing stride, every dimension of more than one
+    element steps past all the offsets the smaller ones reach (the kernels'
+    rule for an output; expanded views break it)."""
+    if tensor.shape[3] > 1 and tensor.stride(3) != 1:
+        return False
+    reach = tensor.shape[3]
+    for size, stride in sorted(zip(tensor.shape[:3], tensor.stride()[:3]), key=lambda d: d[1]):
+        if size <= 1:
+            continue
+        if stride < reach:
+            return False
+        reach += stride * (size - 1)
+    return True
+
+
 def prefill_attention(q, k, v, backend="hip", *, query_start=0, out=None, workspace=None):
     """Causal prefill attention over [batch, heads, tokens, head_dim] tensors.
 
@@ -129,7 +146,8 @@ def prefill_attention(q, k, v, backend="hip", *, query_start=0, out=None, worksp
     tokens, head_dim] tensor is a view of [batch, tokens, q_heads, head_dim]
     storage, so the caller's transpose back to [tokens, heads, head_dim] is
     contiguous.  ``out`` may supply any [batch, q_heads, tokens, head_dim]
-    tensor of q's dtype whose innermost dim is dense.
+    tensor of q's dtype whose innermost dim is dense and whose elements are
+    distinct (not an expanded view).
     """
     if backend != "hip":
         raise ValueError("unknown prefill backend")
@@ -161,6 +179,8 @@ def prefill_attention(q, k, v, backend="hip", *, query_start=0, out=None, worksp
             raise ValueError("out must be a [batch, q_heads, tokens, head_dim] tensor of q's dtype and device")
         if not _dense_layout_ok(out, head_dim):
             raise ValueError("out must have a dense head_dim and 16-byte aligned rows")
+        if not _dense_disjoint(out):
+            raise ValueError("out must not overlap itself")
         result = out
     if min(batch, q_heads, head_dim) == 0:
         return result

@@ -174,11 +174,12 @@ def test_dense_prefill_plan_and_rejections(lib):
     assert lib.dense_prefill_workspace_size(1, 64, 16, 8, 128, 0, 9) == 0
 
     def call(batch=1, q_heads=16, kv_heads=8, tokens=64, kv_tokens=64, head_dim=128, start=0, ptr=256, out=256,
-             q_strides=None, kv_strides=None, dtype=bf16, workspace=None, workspace_bytes=0):
+             q_strides=None, kv_strides=None, out_strides=None, dtype=bf16, workspace=None, workspace_bytes=0):
         q_strides = q_strides or (q_heads * tokens * head_dim, tokens * head_dim, head_dim)
         kv_strides = kv_strides or (kv_heads * kv_tokens * head_dim, kv_tokens * head_dim, head_dim)
+        out_strides = out_strides or (q_heads * tokens * head_dim, tokens * head_dim, head_dim)
         return _status(lib, "mvme_prefill_attention", out, ptr, ptr, ptr, batch, q_heads, kv_heads, tokens, kv_tokens,
-                       head_dim, start, *q_strides, *kv_strides, *q_strides, dtype, workspace, workspace_bytes,
+                       head_dim, start, *q_strides, *kv_strides, *out_strides, dtype, workspace, workspace_bytes,
                        None)
 
     assert call(dtype=7) == ext.EINVAL and "FP16/BF16" in lib.last_error()
@@ -191,6 +192,10 @@ def test_dense_prefill_plan_and_rejections(lib):
     assert call(q_strides=(16 * 64 * 128, 64 * 128, 132)) == ext.EINVAL and "multiples of 8" in lib.last_error()
     assert call(q_strides=(0, -8, 128)) == ext.EINVAL and "strides out of range" in lib.last_error()
     assert call(kv_strides=(1 << 50, 64 * 128, 128), batch=4096) == ext.EINVAL and "out of range" in lib.last_error()
+    # Output rows must be distinct: an expanded head dim, heads 64 elements
+    # apart (inside a 128-element row), tokens overlapping the heads.
+    for strides in ((16 * 64 * 128, 0, 128), (16 * 64 * 128, 64, 64 * 64), (16 * 64 * 128, 128, 8 * 128)):
+        assert call(out_strides=strides) == ext.EINVAL and "overlap" in lib.last_error()
     # A split plan without (or with too small) a workspace.
     assert call(tokens=4096, kv_tokens=4096) == ext.EWORKSPACE and "workspace" in lib.last_error()
     assert call(tokens=4096, kv_tokens=4096, workspace=256, workspace_bytes=1024) == ext.EWORKSPACE

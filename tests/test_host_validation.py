@@ -81,6 +81,23 @@ def test_dense_prefill_contract_on_cpu():
         prefill_attention(q.float(), k.float(), v.float(), query_start=8)
 
 
+def test_dense_prefill_output_must_not_overlap_itself():
+    """A caller's output for prefill_attention is written through its
+    strides, so its elements must be distinct: the rule the wrapper and
+    mvme_prefill_attention apply (by increasing stride, each dimension of
+    more than one element steps past everything the smaller ones reach)."""
+    from mini_engine_hip.kernels.prefill import _dense_disjoint
+
+    assert _dense_disjoint(torch.empty(2, 4, 8, 16))
+    assert _dense_disjoint(torch.empty(2, 8, 4, 16).transpose(1, 2))  # token-major
+    assert _dense_disjoint(torch.empty(1, 1, 1, 16))
+    assert _dense_disjoint(torch.empty(3, 64, 4, 16)[:, ::2].transpose(1, 2))  # gaps are fine
+    assert not _dense_disjoint(torch.empty(2, 1, 8, 16).expand(2, 4, 8, 16))
+    assert not _dense_disjoint(torch.empty(4096).as_strided((1, 4, 8, 16), (512, 8, 64, 1)))
+    assert not _dense_disjoint(torch.empty(4096).as_strided((1, 4, 8, 16), (512, 16, 32, 1)))
+    assert not _dense_disjoint(torch.empty(2, 4, 8, 32)[..., ::2])
+
+
 def test_slot_scatter_rejects_races_before_mutation():
     """test_ragged_kernels.py:48-65: duplicate slots, overlap, capacity."""
     _, key, value, *_ = inputs()
