@@ -1069,9 +1069,11 @@ template <int KEYS, bool DENSE>
 __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta& first) {
     constexpr float kFixed = kItemFixedTiles * 64.f / KEYS;  // an item's fixed cost in tiles of KEYS keys
     const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
-    const int cap = a.table_width * a.block_size;
-    const int cmax = (cap + KEYS - 1) / KEYS * KEYS;
-    const int span = (cmax - a.chunk) / KEYS;  // candidate steps above the minimum
+    // 64-bit: the capacity may be up to 2^31 - 1 keys, and candidates past it
+    // are formed (and rejected) too.
+    const int64_t cap = (int64_t)a.table_width * a.block_size;
+    const int64_t cmax = (cap + KEYS - 1) / KEYS * KEYS;
+    const int span = (int)((cmax - a.chunk) / KEYS);  // candidate steps above the minimum
     uint32_t items = 0, tiles = 0;
     // Up to 64 sequences (lane j of every wave holds sequence j) the key
     // ends of all query blocks go into one list in LDS first, each computed
@@ -1107,8 +1109,9 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
     const int slices = wide ? 1 : kChoiceSlices;
     const int ci = tid % cands, slice = tid / cands;
     const int step = max(1, (span + cands - 1) / cands);
-    const int cand = a.chunk + KEYS * step * ci;
-    const bool valid = cand <= cmax;  // candidate 0, the minimum, always is
+    const int64_t cand64 = a.chunk + (int64_t)KEYS * step * ci;
+    const bool valid = cand64 <= cmax && cand64 <= 2147483647;  // candidate 0, the minimum, always is
+    const int cand = valid ? (int)cand64 : a.chunk;
     if (flat) {
         if (__builtin_amdgcn_ballot_w64(valid) != 0) {  // wave-uniform
             for (int b = slice; b < total_blocks; b += slices) {
@@ -1187,7 +1190,7 @@ __device__ int choose_chunk(const PrefillArgs& a, PrefillLds& lds, const SeqMeta
     __syncthreads();
     uint64_t best = lds.pick[0];
     for (int w = 1; w < pricing_waves; ++w) best = lds.pick[w] < best ? lds.pick[w] : best;
-    return a.chunk + KEYS * step * (int)(uint32_t)best;
+    return (int)(a.chunk + (int64_t)KEYS * step * (int)(uint32_t)best);  // a valid candidate: below 2^31
 }
 
 // Items are enumerated densely.  WALK = false: one item per work-group (the
