@@ -10,14 +10,15 @@ which chunk the device took.  Two checks pin it:
   picks;
 * the call gives the same bits as a call given that chunk explicitly.
 
-The model (restated from the kernel): candidates are the host's chunk
-max(512, capacity/32 rounded up to 64 keys) plus multiples of 64*step keys,
-128 of them (512 with fewer than 16 query blocks) up to the capacity; each
-costs
-max(ceil(items/W) * (5 + chunk/64), (tiles + 5 * items) / W) in fp32 with
-W = 256 / kv_heads work-groups per kv head; the cheapest wins, ties going to
-the smaller chunk.  The choice is made only when the host's chunk gives more
-than one round of items.
+The model (restated from the kernel), with K keys per tile (64 for head
+dims up to 128, 32 above) and query blocks of 256 rows (128 above 128):
+candidates are the host's chunk max(512, capacity/32 rounded up to K keys)
+plus multiples of K*step keys, 128 of them (512 with fewer than 16 query
+blocks) up to the capacity; each costs
+max(ceil(items/W) * (F + chunk/K), (tiles + F * items) / W) in fp32 with
+F = 5 * 64 / K tiles and W = 256 / kv_heads work-groups per kv head; the
+cheapest wins, ties going to the smaller chunk.  The choice is made only when
+the host's chunk gives more than one round of items.
 """
 
 import numpy as np
@@ -32,7 +33,6 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 CUS = 256
 KEYS = 64
-FIXED = np.float32(5.0)
 NAMES = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
 PRIORS8 = [2220, 601, 877, 1126, 1381, 3550, 2532, 347]
 
@@ -45,14 +45,16 @@ def block_ends(priors, new_tokens, qb, cap):
     return [min(p + min(q0 + qb, new_tokens), cap) for p in priors for q0 in range(0, new_tokens, qb)]
 
 
-def model_chunk(priors, new_tokens, block_size, table_width, q_heads, kv_heads):
-    qb = 256 // (q_heads // kv_heads)
+def model_chunk(priors, new_tokens, block_size, table_width, q_heads, kv_heads, head_dim=128):
+    keys = KEYS if head_dim <= 128 else KEYS // 2
+    fixed = np.float32(5.0 * 64 / keys)
+    qb = (256 if head_dim <= 128 else 128) // (q_heads // kv_heads)
     cap = table_width * block_size
-    host = max(512, ceil_div(ceil_div(cap, 32), KEYS) * KEYS)
-    cmax = ceil_div(cap, KEYS) * KEYS
+    host = max(512, ceil_div(ceil_div(cap, 32), keys) * keys)
+    cmax = ceil_div(cap, keys) * keys
     ends = block_ends(priors, new_tokens, qb, cap)
     cands = 512 if len(priors) <= 64 and len(ends) < 16 else 128
-    step = max(1, ceil_div((cmax - host) // KEYS, cands))
+    step = max(1, ceil_div((cmax - host) // keys, cands))
     w = max(1, CUS // kv_heads)
 
     def items(c):
@@ -60,16 +62,16 @@ def model_chunk(priors, new_tokens, block_size, table_width, q_heads, kv_heads):
 
     if items(host) <= w:
         return host, False
-    tiles = sum(ceil_div(e, KEYS) for e in ends)
+    tiles = sum(ceil_div(e, keys) for e in ends)
     best = None
     for i in range(cands):
-        c = host + KEYS * step * i
+        c = host + keys * step * i
         if c > cmax:
             break
         n = items(c)
         rounds = np.float32(ceil_div(n, w))
-        cost = max(rounds * (FIXED + np.float32(c // KEYS)),
-                   (np.float32(tiles) + FIXED * np.float32(n)) / np.float32(w))
+        cost = max(rounds * (fixed + np.float32(c // keys)),
+                   (np.float32(tiles) + fixed * np.float32(n)) / np.float32(w))
         if best is None or cost < best[0]:
             best = (cost, c)
     return best[1], True
@@ -98,8 +100,17 @@ def test_device_choice_matches_the_model(num_seqs, new_tokens, priors):
     print(f"chunk choice {num_seqs}x{new_tokens}: model {want} (choice made: {chose})", flush=True)
     assert chose, "shape must need more than one round of items at the host's chunk"
 
+    check_choice(args, priors, new_tokens, want)
+
+
+def check_choice(args, priors, new_tokens, want):
+    """The device's chunk counts are those of `want`, and the call equals one given `want`."""
+    q, kc, tables = args[0], args[1], args[5]
+    tokens, q_heads = q.shape[0], q.shape[1]
+    _, block_size, kv_heads, head_dim = kc.shape
+    width = tables.shape[1]
     lib = ext.load_hip_extension()
-    need = lib.prefill_workspace_size(num_seqs, tokens, q_heads, kv_heads, head_dim, block_size, width, 0,
+    need = lib.prefill_workspace_size(len(priors), tokens, q_heads, kv_heads, head_dim, block_size, width, 0,
                                       ext.dtype_code(q.dtype))
     workspace = torch.zeros(need, dtype=torch.uint8, device=DEV)
     auto = paged_prefill_attention(*args, block_size, backend="hip", validate=False, workspace=workspace)
@@ -108,7 +119,7 @@ def test_device_choice_matches_the_model(num_seqs, new_tokens, priors):
 
     tok_bytes = (tokens * 4 + 15) // 16 * 16
     counts = workspace[need - tok_bytes:need - tok_bytes + tokens * 4].cpu().view(torch.int32).tolist()
-    qb = 256 // (q_heads // kv_heads)
+    qb = (256 if head_dim <= 128 else 128) // (q_heads // kv_heads)
     expected = []
     for p in priors:
         for t in range(new_tokens):
@@ -116,3 +127,24 @@ def test_device_choice_matches_the_model(num_seqs, new_tokens, priors):
             expected.append(ceil_div(end, want))
     assert counts == expected
     assert torch.equal(auto, explicit)
+
+
+def test_head_dim_256_tiles_of_32_keys():
+    """Head dim 256: 32-key tiles (an item's fixed cost is 10 of them) and
+    query blocks of 128 rows (64 tokens at GQA 2).  One 2048-token prompt,
+    Hq8/Hkv4: 80 items at the host's 512-key chunk against 64 work-groups
+    per kv head, so the device chooses."""
+    gen = torch.Generator().manual_seed(256)
+    tokens, q_heads, kv_heads, head_dim, block = 2048, 8, 4, 256, 256
+    pages = tokens // block
+    perm = torch.randperm(pages + 3, generator=gen)[:pages]
+    tables = perm.view(1, pages).to(torch.int64)
+    kc = torch.randn(pages + 3, block, kv_heads, head_dim, generator=gen).to(torch.bfloat16)
+    vc = torch.randn(pages + 3, block, kv_heads, head_dim, generator=gen).to(torch.bfloat16)
+    q = torch.randn(tokens, q_heads, head_dim, generator=gen).to(torch.bfloat16)
+    meta = (torch.tensor([0, tokens]), torch.tensor([0]), tables, torch.tensor([tokens]))
+    args = [t.to(DEV) for t in (q, kc, vc, *meta)]
+    want, chose = model_chunk([0], tokens, block, pages, q_heads, kv_heads, head_dim)
+    print(f"chunk choice D=256 1x{tokens}: model {want} (choice made: {chose})", flush=True)
+    assert chose
+    check_choice(args, [0], tokens, want)
