@@ -148,3 +148,31 @@ def test_head_dim_256_tiles_of_32_keys():
     print(f"chunk choice D=256 1x{tokens}: model {want} (choice made: {chose})", flush=True)
     assert chose
     check_choice(args, [0], tokens, want)
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_dense_prefill_chooses_like_the_paged_walk(batch):
+    """prefill_attention's dense mode: each batch entry is a sequence whose
+    keys are one page of the context rounded up to a power of two (2048
+    here), and the walk chooses its chunk by the same model."""
+    from mini_engine_hip.kernels.prefill import prefill_attention
+
+    tokens, q_heads, kv_heads, head_dim = 2048, 16, 8, 128
+    gen = torch.Generator().manual_seed(batch)
+    q = torch.randn(batch, q_heads, tokens, head_dim, generator=gen).to(torch.bfloat16).to(DEV)
+    k = torch.randn(batch, kv_heads, tokens, head_dim, generator=gen).to(torch.bfloat16).to(DEV)
+    v = torch.randn(batch, kv_heads, tokens, head_dim, generator=gen).to(torch.bfloat16).to(DEV)
+    want, chose = model_chunk([0] * batch, tokens, tokens, 1, q_heads, kv_heads)
+    print(f"dense chunk choice {batch}x{tokens}: model {want} (choice made: {chose})", flush=True)
+    assert chose
+    lib = ext.load_hip_extension()
+    need = lib.dense_prefill_workspace_size(batch, tokens, q_heads, kv_heads, head_dim, 0, ext.dtype_code(q.dtype))
+    workspace = torch.zeros(need, dtype=torch.uint8, device=DEV)
+    prefill_attention(q, k, v, "hip", workspace=workspace)
+    torch.cuda.synchronize()
+    rows = batch * tokens
+    tok_bytes = (rows * 4 + 15) // 16 * 16
+    counts = workspace[need - tok_bytes:need - tok_bytes + rows * 4].cpu().view(torch.int32).tolist()
+    qb = 256 // (q_heads // kv_heads)
+    expected = [ceil_div(min(t // qb * qb + qb, tokens), want) for _ in range(batch) for t in range(tokens)]
+    assert counts == expected
