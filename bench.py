@@ -397,6 +397,7 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra)
     if "prefill" in names:
         _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra)
+        _extra_prefill_cold(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra)
     if "prefill_shapes" in names:
         _extra_prefill_shapes(torch, write_kv_cache_slots, paged_prefill_attention, workloads, dev, extra)
     if "dense_prefill" in names:
@@ -530,6 +531,52 @@ def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloa
         "algorithmic_bytes": kv_bytes, "roofline_bound_us": bound_s * 1e6,
         "frac_of_roofline_time": bound_s / per_call, "flops": flops, "priors": c["priors"],
         "max_abs_error": err}
+
+
+def _extra_prefill_cold(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra):
+    """The 8 x 128 chunked prefill with its inputs cold: 8 separately
+    allocated workloads (same priors, different data; about 63 MB of K/V
+    pages each, 500 MB together, twice the 256 MB Infinity Cache) are cycled
+    in one graph, as the headline cycles 28 layer pools, so that no call finds
+    its pages in the cache a previous call left them in.  One workspace,
+    sized for the call, serves every call (what a layer loop does)."""
+    from mini_engine_hip.kernels.prefill import paged_prefill_workspace_bytes
+
+    names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+    priors = [2220, 601, 877, 1126, 1381, 3550, 2532, 347]
+    cases = []
+    for i in range(8):
+        c = workloads.chunked_prefill_case(device=dev, seed=BASE_SEED + 40 + i, priors=priors)
+        write_kv_cache_slots(c["key_cache"], c["value_cache"], c["slot_mapping"], c["new_key"], c["new_value"],
+                             backend="hip", validate=False)
+        cases.append([c[n] for n in names])
+    q, kc = cases[0][0], cases[0][1]
+    need = paged_prefill_workspace_bytes(len(priors), q.shape[0], q.shape[1], kc.shape[2], q.shape[2], 256,
+                                         cases[0][5].shape[1], q.dtype)
+    workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+    outs = [None] * len(cases)
+
+    def cycle():
+        for i, pargs in enumerate(cases):
+            outs[i] = paged_prefill_attention(*pargs, 256, backend="hip", validate=False, workspace=workspace)
+
+    ms, _ = graph_time_ms(cycle, torch, calls_per_graph=len(cases), replays=10, warmup=2)
+    per_call = ms / len(cases) * 1e-3
+    flops = workloads.prefill_flops(priors)
+    kv_bytes = sum(p + 128 for p in priors) * 4096 + 2 * 1024 * 16 * 128 * 2
+    bound_s = max(flops / (MFMA_BF16_PEAK_TFLOPS * 1e12), kv_bytes / (HBM_PEAK_GBS * 1e9))
+    errs = None
+    if cpu is not None:
+        errs = max(max_abs(outs[i], cpu.prefill(*[a.cpu() for a in cases[i]], 256, cast=False)) for i in (0, 7))
+    extra["chunked_prefill_8x128_bf16_cold"] = {
+        "us_per_call": per_call * 1e6, "TFLOPs": flops / per_call / 1e12,
+        "frac_of_bf16_mfma_peak": flops / per_call / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "GBps": kv_bytes / per_call / 1e9, "frac_of_hbm_peak": kv_bytes / per_call / 1e9 / HBM_PEAK_GBS,
+        "roofline_bound_us": bound_s * 1e6, "frac_of_roofline_time": bound_s / per_call,
+        "workloads_cycled": len(cases), "distinct_kv_bytes": sum(a[1].numel() * 4 for a in cases),
+        "max_abs_error_calls_0_and_7": errs}
+    del cases, outs, workspace
+    torch.cuda.empty_cache()
 
 
 def _extra_prefill_shapes(torch, write_kv_cache_slots, paged_prefill_attention, workloads, dev, extra):

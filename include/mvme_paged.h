@@ -178,7 +178,10 @@ int mvme_paged_attention_noalloc(void* out, const void* query,
  *     and the V row new_value, and the attention query is
  *     rope(rmsnorm(query, q_weight), cos, sin) of the raw query rows
  *     (query_token_stride elements apart); the rotated queries also go to
- *     q_out ([batch, q_heads, head_dim]) when it is not NULL.  cos / sin are
+ *     q_out ([batch, q_heads, head_dim]) when it is not NULL; q_out must
+ *     not overlap the raw query rows (MVME_EINVAL: every work-group reads
+ *     them while the first writes q_out; rotate in place with
+ *     mvme_qk_norm_rope_write_kv instead).  cos / sin are
  *     [batch, head_dim / 2] at each sequence's position; eps the RMSNorm eps.
  * Then attention over context_lens[b] tokens exactly as mvme_paged_attention
  * (same workspace).  Results equal the two-launch sequence

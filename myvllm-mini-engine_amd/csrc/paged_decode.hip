@@ -413,6 +413,18 @@ extern "C" int mvme_paged_attention_decode_write(
                                     aligned16(sin) && query_token_stride % 8 == 0 &&
                                     (q_out == nullptr || aligned16(q_out))));
     if (!aligned) return fail(MVME_EINVAL, "paged decode with KV write needs 16-byte aligned rows");
+    if (rope && q_out != nullptr) {
+        // Every wave (and every split-K partition) reads the raw query rows
+        // while the first partition writes the rotated rows to q_out, so the
+        // two byte ranges must be disjoint (an in-place rotation belongs to
+        // the two-launch sequence).
+        const uintptr_t q_lo = reinterpret_cast<uintptr_t>(query);
+        const uintptr_t q_hi = q_lo + (uintptr_t)(((batch - 1) * query_token_stride + q_heads * head_dim) * 2);
+        const uintptr_t o_lo = reinterpret_cast<uintptr_t>(q_out);
+        const uintptr_t o_hi = o_lo + (uintptr_t)(batch * q_heads * head_dim * 2);
+        if (o_lo < q_hi && q_lo < o_hi)
+            return fail(MVME_EINVAL, "q_out must not overlap the raw query rows");
+    }
     const size_t need = mvme_paged_attention_workspace_size(batch, q_heads, kv_heads, head_dim, block_size,
                                                             table_width, partition_tokens);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need))

@@ -150,9 +150,14 @@ class PrefillBatch:
             raise ValueError("token IDs must be nonnegative")
         table = _padded_tables(rows)
         pages_per_row = _table_pages(table, num_blocks)
-        ends = start + lengths
-        if bool((ends > pages_per_row * block_size).any()):
+        # Python ints: a start near 2^63 or a huge block_size must not wrap
+        # around in int64 and slip past the capacity rule.
+        if any(s + len(seq) > pages * block_size
+               for s, seq, pages in zip(starts, sequences, pages_per_row.tolist())):
             raise ValueError("query range exceeds supplied block table capacity")
+        if num_blocks * block_size > _INT64[1]:
+            raise ValueError("KV slots (num_blocks * block_size) must fit int64")
+        ends = start + lengths
 
         # Positions and slots of every packed token.
         owner = torch.arange(len(sequences)).repeat_interleave(lengths)

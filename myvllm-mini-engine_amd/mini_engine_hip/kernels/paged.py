@@ -168,6 +168,12 @@ def paged_attention_decode_write(query, key_cache, value_cache, block_tables, co
         _check(not any(torch._C._overlaps(cache, src) for cache in (key_cache, value_cache)
                        for src in (query, new_key, new_value)),
                "KV destinations and source tensors must not overlap")
+    # One launch reads the raw query rows in every work-group while the first
+    # writes q_out, so an overlapping q_out takes the two launches; only an
+    # exact in-place rotation (q_out is the contiguous query) is defined there.
+    in_place = rope and q_out is not None and torch._C._overlaps(q_out, query)
+    if in_place and not (q_out.data_ptr() == query.data_ptr() and query.is_contiguous()):
+        raise ValueError("q_out must be the query itself or not overlap it")
     num_blocks, _, kv_heads, _ = key_cache.shape
     width = block_tables.shape[1]
     q_stride, q_src = _row_stride(query) if rope else (q_heads * head_dim, query)
@@ -184,7 +190,8 @@ def paged_attention_decode_write(query, key_cache, value_cache, block_tables, co
                and sin.dtype == query.dtype and cos.device == query.device and sin.device == query.device,
                "RoPE cos/sin shape mismatch")
         pointers += [q_weight, k_weight, cos, sin] + ([q_out] if q_out is not None else [])
-    fused = (head_dim in FUSED_WRITE_HEAD_DIMS and all(t.data_ptr() % 16 == 0 for t in pointers)
+    fused = (not in_place and head_dim in FUSED_WRITE_HEAD_DIMS
+             and all(t.data_ptr() % 16 == 0 for t in pointers)
              and q_stride % 8 == 0 and k_stride % 8 == 0 and v_stride % 8 == 0)
     if not fused:
         positions = context_lens - 1

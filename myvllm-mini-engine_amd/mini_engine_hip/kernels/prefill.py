@@ -20,6 +20,17 @@ from . import hip_extension as ext
 MAX_HEAD_DIM = 1024
 
 
+def paged_prefill_workspace_bytes(num_seqs, total_tokens, q_heads, kv_heads, head_dim, block_size, table_width,
+                                  dtype, chunk_tokens=0):
+    """Bytes of the key-chunk workspace paged_prefill_attention needs for
+    these shapes (from shapes only: lengths stay on the device).  A layer
+    loop sizes one buffer for its largest call and passes it to every call
+    as ``workspace=``; 0 means the call never splits keys."""
+    return ext.load_hip_extension().prefill_workspace_size(num_seqs, total_tokens, q_heads, kv_heads, head_dim,
+                                                           block_size, table_width, chunk_tokens,
+                                                           ext.dtype_code(dtype))
+
+
 def paged_prefill_attention(q, key_cache, value_cache, cu_seqlens_q, query_starts,
                             block_tables, context_lens, block_size, *, backend="hip", validate=True,
                             chunk_tokens=0, workspace=None):
@@ -117,6 +128,12 @@ def _dense_layout_ok(tensor, head_dim):
     return tensor.data_ptr() % 16 == 0 and all(st % 8 == 0 for st in _dense_strides(tensor))
 
 
+def _aligned_copy(tensor):
+    """A new contiguous copy (the caching allocator's blocks are 16-byte
+    aligned, so its rows meet the MFMA path's alignment)."""
+    return torch.empty_like(tensor, memory_format=torch.contiguous_format).copy_(tensor)
+
+
 def _dense_disjoint(tensor):
     """No two elements of a [batch, heads, tokens, head_dim] tensor share an
     address: taken by increasing stride, every dimension of more than one
@@ -168,10 +185,12 @@ def prefill_attention(q, k, v, backend="hip", *, query_start=0, out=None, worksp
         raise ValueError("HIP prefill supports head_dim up to 1024")
     if query_start + tokens > MAX_DENSE_CONTEXT:
         raise ValueError("HIP prefill supports at most 1048576 context tokens")
+    # A fresh copy, not .contiguous(): a tensor that is already contiguous but
+    # starts at a misaligned storage offset would come back unchanged.
     if not _dense_layout_ok(q, head_dim):
-        q = q.contiguous()
+        q = _aligned_copy(q)
     if k.stride() != v.stride() or not _dense_layout_ok(k, head_dim) or not _dense_layout_ok(v, head_dim):
-        k, v = k.contiguous(), v.contiguous()
+        k, v = _aligned_copy(k), _aligned_copy(v)
     if out is None:
         result = torch.empty(batch, tokens, q_heads, head_dim, dtype=q.dtype, device=q.device).transpose(1, 2)
     else:

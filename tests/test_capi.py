@@ -102,12 +102,13 @@ def test_decode_write_rejects_before_touching_the_device(lib):
     """The fused KV-write decode entry checks shapes, pointers, head_dim,
     norm inputs, strides and alignment before any HIP call."""
     def call(head_dim=128, q_weight=None, k_weight=None, cos=None, sin=None, eps=1e-6, k_stride=None,
-             q_stride=None, ptr=256, new_k=256):
+             q_stride=None, ptr=256, new_k=256, query=None, q_out=None, parts=0, width=2):
         k_stride = 8 * head_dim if k_stride is None else k_stride
         q_stride = 16 * head_dim if q_stride is None else q_stride
-        return _status(lib, "mvme_paged_attention_decode_write", ptr, ptr, ptr, ptr, ptr, ptr, 2, 16, 8, head_dim,
-                       4, 16, 2, 0, 0, new_k, ptr, k_stride, 8 * head_dim, q_weight, k_weight, cos, sin, eps,
-                       q_stride, None, None, 0, None)
+        query = ptr if query is None else query
+        return _status(lib, "mvme_paged_attention_decode_write", ptr, query, ptr, ptr, ptr, ptr, 2, 16, 8,
+                       head_dim, 4, 16, width, parts, 0, new_k, ptr, k_stride, 8 * head_dim, q_weight, k_weight, cos, sin,
+                       eps, q_stride, q_out, None, 0, None)
 
     assert call(head_dim=80) == ext.EINVAL and "16,32,64,128,256" in lib.last_error()
     assert call(new_k=None) == ext.EINVAL and "null pointer" in lib.last_error()
@@ -119,6 +120,15 @@ def test_decode_write_rejects_before_touching_the_device(lib):
     assert "stride" in lib.last_error()
     assert call(ptr=258) == ext.EINVAL and "16-byte aligned" in lib.last_error()
     assert call(k_stride=8 * 128 + 4) == ext.EINVAL and "16-byte aligned" in lib.last_error()
+    # q_out must not overlap the raw query rows (2 tokens, 3072 elements apart,
+    # 2048 elements each): every work-group reads them while one writes q_out.
+    rope = dict(q_weight=256, k_weight=256, cos=256, sin=256, q_stride=3072, query=1 << 20)
+    for q_out in ((1 << 20), (1 << 20) + (3072 + 2048) * 2 - 16, (1 << 20) - 2 * 2 * 2048 + 16):
+        assert call(**rope, q_out=q_out) == ext.EINVAL and "overlap" in lib.last_error()
+    # Adjacent ranges are disjoint: the call passes the overlap check and
+    # stops at the next one, the missing workspace of a split plan.
+    for q_out in ((1 << 20) + (3072 + 2048) * 2, (1 << 20) - 2 * 2 * 2048):
+        assert call(**rope, q_out=q_out, parts=16, width=8) == ext.EWORKSPACE
 
 
 def test_scatter_and_prefill_reject_bad_arguments(lib):
@@ -258,3 +268,19 @@ def test_argmax_workspace_plan(lib):
     assert status == ext.EWORKSPACE and "workspace" in lib.last_error()
     assert lib._lib.mvme_greedy_argmax(1, 1, 2, 10, 9, 1, None, 0, None) == ext.EINVAL
     assert lib._lib.mvme_greedy_argmax(1, 1, 2, 10, 10, 7, None, 0, None) == ext.EINVAL
+
+
+def test_prefill_workspace_bytes_helper(lib):
+    """The Python sizing helper a layer loop uses for its one shared buffer is
+    the library's plan: the 8 x 128 bf16 batch (capacity 4096 keys, 512-key
+    chunks, 8 chunk planes of 1024 tokens x 16 heads x (256 + 8) bytes, plus
+    one int per token); fp16 keeps fp32 partials."""
+    import torch
+
+    from mini_engine_hip.kernels.prefill import paged_prefill_workspace_bytes
+
+    bf16 = paged_prefill_workspace_bytes(8, 1024, 16, 8, 128, 256, 16, torch.bfloat16)
+    assert bf16 == lib.prefill_workspace_size(8, 1024, 16, 8, 128, 256, 16, 0, ext.dtype_code(torch.bfloat16))
+    assert 8 * 1024 * 16 * (256 + 8) + 4096 <= bf16 < 8 * 1024 * 16 * (256 + 8) + 4096 + 64
+    fp16 = paged_prefill_workspace_bytes(8, 1024, 16, 8, 128, 256, 16, torch.float16)
+    assert 8 * 1024 * 16 * (512 + 8) + 4096 <= fp16 < 8 * 1024 * 16 * (512 + 8) + 4096 + 64

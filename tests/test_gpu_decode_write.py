@@ -125,7 +125,7 @@ def test_split_k_and_head_dims(rope, head_dim):
     step = make_step(2, 8, 2, head_dim, 16, [1500, 777], torch.bfloat16, seed=head_dim)
     print(f"decode write split-K rope={rope} D={head_dim}", flush=True)
     check_equal(step, 16, rope, partition_tokens=256)
-    check_equal(step, 16, rope, partition_tokens=0, oracle=False)
+    check_equal(step, 16, rope, partition_tokens=0)
 
 
 @pytest.mark.parametrize("q_heads,kv_heads", [(8, 8), (32, 8), (64, 8), (28, 4)])
@@ -134,7 +134,7 @@ def test_gqa_tiles(q_heads, kv_heads):
     step = make_step(6, q_heads, kv_heads, 128, 32, [5, 300, 64, 1, 129, 700], torch.float16, seed=q_heads)
     print(f"decode write GQA {q_heads}/{kv_heads}", flush=True)
     check_equal(step, 32, True)
-    check_equal(step, 32, False, oracle=False)
+    check_equal(step, 32, False)
 
 
 def test_strided_fused_qkv_rows():
@@ -143,7 +143,7 @@ def test_strided_fused_qkv_rows():
     requires."""
     step = make_step(8, 16, 8, 128, 16, [33, 17, 1, 250, 96, 7, 128, 64], torch.bfloat16, seed=5, fused_qkv=True)
     check_equal(step, 16, True)
-    check_equal(dict(step, q=step["q"].contiguous()), 16, False, oracle=False)
+    check_equal(dict(step, q=step["q"].contiguous()), 16, False)
 
 
 def test_absent_page_is_not_written():
@@ -166,7 +166,7 @@ def test_other_head_dims_run_two_launches():
     attention as two launches and gives the same results."""
     step = make_step(3, 8, 4, 80, 16, [20, 3, 57], torch.float16, seed=80)
     check_equal(step, 16, True)
-    check_equal(step, 16, False, oracle=False)
+    check_equal(step, 16, False)
 
 
 def test_trusted_empty_context_and_no_q_out():
@@ -181,3 +181,31 @@ def test_trusted_empty_context_and_no_q_out():
     torch.cuda.synchronize()
     assert torch.equal(kc, want_k) and torch.equal(vc, want_v) and torch.equal(got, want_out)
     assert not got[0].any()
+
+
+def test_in_place_rotation_takes_two_launches():
+    """q_out that is the query itself (an in-place rotation) runs the two
+    launches, whose norm/RoPE kernel reads and writes each row in the same
+    lanes; a q_out that overlaps the query any other way is refused (one
+    launch reads the raw rows in every work-group while another writes
+    q_out)."""
+    step = make_step(4, 16, 8, 128, 16, [40, 9, 300, 77], torch.bfloat16, seed=31)
+    want_k, want_v, want_q, want_out = two_launches(step, 16, True, 0)
+    kc, vc = step["kc"].clone(), step["vc"].clone()
+    q = step["q"].clone()
+    got = paged_attention_decode_write(q, kc, vc, step["tables"], step["lens"], 16, step["k"], step["v"],
+                                       q_out=q, **step["norm"])
+    torch.cuda.synchronize()
+    assert torch.equal(kc, want_k) and torch.equal(vc, want_v)
+    assert torch.equal(q, want_q) and torch.equal(got, want_out)
+    tensors = dict(zip(paged_oracle.TENSOR_NAMES, (q.cpu(), kc.cpu(), vc.cpu(), step["tables"].cpu(),
+                                                    step["lens"].cpu())))
+    want = paged_oracle.fp32_oracle(tensors, 16)
+    assert (got.float().cpu() - want).abs().max().item() <= GATE[torch.bfloat16]
+    # A q_out shifted by one query row overlaps the query without being it.
+    storage = torch.empty(5 * 16 * 128, dtype=torch.bfloat16, device=DEV)
+    raw = storage[:4 * 16 * 128].view(4, 16, 128).copy_(step["q"])
+    shifted = storage[16 * 128:].view(4, 16, 128)
+    with pytest.raises(ValueError, match="overlap"):
+        paged_attention_decode_write(raw, step["kc"].clone(), step["vc"].clone(), step["tables"], step["lens"], 16,
+                                     step["k"], step["v"], q_out=shifted, **step["norm"])

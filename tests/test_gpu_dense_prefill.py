@@ -156,3 +156,22 @@ def test_sliced_views_differing_kv_strides_and_graph_replay():
         torch.cuda.synchronize()
         assert torch.equal(static_out, eager), step
         check(static_out, q, k, v, 250, dtype)
+
+
+def test_misaligned_contiguous_inputs_are_copied():
+    """Contiguous q/k/v that start one element into their storage (so their
+    rows are not 16-byte aligned) are served through aligned copies instead of
+    being refused by the MFMA path."""
+    gen = torch.Generator().manual_seed(919)
+    dtype = torch.bfloat16
+
+    def shifted(*shape):
+        flat = randn(gen, 1 + torch.Size(shape).numel(), dtype=dtype)
+        return flat[1:].view(*shape)
+
+    q, k, v = shifted(1, 16, 40, 128), shifted(1, 8, 72, 128), shifted(1, 8, 72, 128)
+    assert q.is_contiguous() and q.data_ptr() % 16 != 0
+    print("dense prefill misaligned contiguous inputs", flush=True)
+    out = prefill_attention(q, k, v, "hip", query_start=32)
+    torch.cuda.synchronize()
+    check(out, q, k, v, 32, dtype)

@@ -190,6 +190,19 @@ def test_prefill_metadata_rejects_invalid_layout(sequences, tables, starts, erro
         metadata(sequences, tables, starts)
 
 
+@pytest.mark.parametrize("starts,block_size,error", [
+    ([(1 << 63) - 1], 4, "capacity"),        # start + length wraps around in int64
+    ([(1 << 63) - 2], 1 << 62, "fit int64"),  # inside the capacity, but slots cannot be int64
+    ([0], 1 << 64, "fit int64"),             # block_size beyond int64
+])
+def test_prefill_metadata_rejects_int64_wraparound(starts, block_size, error):
+    """Range rules are checked on Python integers: values near 2^63 raise the
+    reference's ValueError instead of wrapping around (or an IndexError)."""
+    with pytest.raises(ValueError, match=error):
+        PrefillBatch.from_sequences([[1, 2]], [[0, 1]], starts, block_size=block_size, num_blocks=16,
+                                    device="cpu")
+
+
 @pytest.mark.parametrize("seed", range(6))
 def test_prefill_metadata_matches_oracle_on_random_batches(seed):
     """Ragged batches whose requests share read-only prefix pages: every field
