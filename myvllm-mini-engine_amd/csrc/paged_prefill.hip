@@ -513,6 +513,8 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                                                             PrefillLds& lds) {
     using SH = PfShape<HD>;
     constexpr bool SCALAR_PAGES = PAGES != kPagesPerLane;
+    // The software-pipelined loop serves whole-tile pages of the 128 shape.
+    constexpr bool PIPE = PAGES == kPagesPerTile && !NARROW && HD == 128 && !DENSE;
     const int hd = NARROW ? a.head_dim : SH::kD;  // elements per K/V/Q/output row in memory
     const int dchunks = hd / 8;                 // 16-byte chunks per row
     auto& sm_k = lds.k;
@@ -766,6 +768,308 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
     for (int nb = 0; nb < SH::kNb; ++nb)
         out_off[nb] = DENSE ? seq * a.o_seq + (row0 + qi[nb]) * a.o_tok + head[nb] * a.o_head : 0;
 
+    // Row sums accumulated on the matrix core (pipelined loop only): a
+    // block of ones times P^T gives every lane its row's full sum.
+    f32x4 osum[SH::kNb];
+#pragma unroll
+    for (int nb = 0; nb < SH::kNb; ++nb) osum[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if constexpr (PIPE) {
+        // Software-pipelined tile loop.  Step i computes S^T of tile i+1,
+        // then O^T += V^T P^T of tile i, then the probabilities of tile
+        // i+1, so each wave's products of two tiles run back to back and the
+        // softmax of one tile follows the products of the previous one.  K
+        // is therefore needed one tile before V: the K copies run one tile
+        // ahead of the V copies, both in 4-stage rings (tile i: K and V
+        // stage i mod 4, i counted from t_begin).
+        //
+        // The queries are pre-scaled by scale*log2(e) and each score product
+        // starts from the row's -reference (the MFMA's C input), so a
+        // probability is one exp2 of the product.
+        const u32x4 ones = {T::pack(1.f, 1.f), T::pack(1.f, 1.f), T::pack(1.f, 1.f), T::pack(1.f, 1.f)};
+        const int ntiles = t_end - t_begin;
+        f32x4 sc[SH::kHalves][SH::kNb][2];
+        u32x4 pops[SH::kHalves][SH::kNb];
+        // Per lane j: byte offset (from the kv head's base) of tile
+        // tile_base + j's first key row when the tile is whole (present page,
+        // all of its keys in the chunk), else -1.
+        int64_t tile_offs = -1;
+        auto window_offsets = [&](int64_t raw, int base) -> int64_t {
+            const int key0 = (base + lane) * SH::kKeys;
+            const bool whole = raw >= 0 && raw < a.num_blocks && key0 + SH::kKeys <= chunk_end;
+            return whole ? raw * page_bytes_g + (int64_t)(key0 & (a.block_size - 1)) * row_bytes_g : (int64_t)-1;
+        };
+        // Moves to the next window (loaded a window ago, retired by a landed
+        // barrier's full wait since) and loads the one after it.  Called at
+        // one place per issue phase: two consecutive tiles never both cross
+        // a window boundary, and a second call site would read the load the
+        // first one just issued.
+        auto next_window = [&]() {
+            tile_pages = next_pages;
+            tile_base += kWave;
+            tile_offs = window_offsets(tile_pages, tile_base);
+            if (tile_base + kWave < t_end) next_pages = window_pages(tile_base + kWave);
+        };
+        // Row-by-row copies of a tile that is not whole: absent rows load
+        // zeros (finite in both rings) and, for K, get a -inf bias.
+        auto issue_rows = [&](int tile, int st, bool is_k) {
+            const int key0 = tile * SH::kKeys;
+            const int64_t page = ctable[(key0 < cap ? key0 : cap - 1) >> bs_shift];
+            const bool pg_ok = key0 < chunk_end && page >= 0 && page < a.num_blocks;
+            const int64_t base = pg_ok ? page * page_bytes_g : 0;
+            const uint8_t* cache = is_k ? kcache : vcache;
+            const uint32_t lds0 = lds_addr(is_k ? &sm_k[st][0] : &sm_v[st][0]);
+#pragma unroll
+            for (int i = 0; i < SH::kIpw; ++i) {
+                const int j = SH::kIpw * wave + i;
+                const int row = SH::kRowsPerInst * j + lrow;
+                const int key = key0 + row;
+                const int cidx = is_k ? lslot ^ (row & 15) : lslot ^ ((2 * row) & 15);
+                const bool ok = pg_ok && key < chunk_end;
+                const uint8_t* g = reinterpret_cast<const uint8_t*>(kZeroChunk);
+                if (ok) g = cache + base + (int64_t)(key & (a.block_size - 1)) * row_bytes_g + 16 * cidx;
+                lds_dma16(g, lds0 + 1024 * j);
+                if (is_k && lslot == 0) sm_b[st][row] = ok ? 0.f : kNegInf;
+            }
+        };
+        auto issue_k = [&](int tile, int st, int64_t off) {
+            if (off >= 0) {
+                full_stages |= 1u << st;
+                const uint32_t lk = lds_addr(&sm_k[st][0]);
+#pragma unroll
+                for (int i = 0; i < SH::kIpw; ++i) lds_dma16_s(kcache + off, tile_off[i], lk + 1024 * (SH::kIpw * wave + i));
+            } else {
+                full_stages &= ~(1u << st);
+                issue_rows(tile, st, true);
+            }
+        };
+        auto issue_v = [&](int tile, int st, int64_t off) {
+            if (off >= 0) {
+                const uint32_t lv = lds_addr(&sm_v[st][0]);
+#pragma unroll
+                for (int i = 0; i < SH::kIpw; ++i)
+                    lds_dma16_s(vcache + off, tile_off_v[i], lv + 1024 * (SH::kIpw * wave + i));
+            } else {
+                issue_rows(tile, st, false);
+            }
+        };
+        // S^T of a tile (K stage st), starting from -reference.
+        auto s_product = [&](int st) __attribute__((always_inline)) {
+            const uint8_t* smk = &sm_k[st][0];
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int h = 0; h < SH::kHalves; ++h) {
+                u32x4 kop[2][SH::kDc];
+#pragma unroll
+                for (int dc = 0; dc < SH::kDc; ++dc) {
+                    kop[0][dc] = *reinterpret_cast<const u32x4*>(smk + 32 * h * SH::kRowBytes + koff[dc]);
+                    kop[1][dc] = *reinterpret_cast<const u32x4*>(smk + (32 * h + 16) * SH::kRowBytes + koff[dc]);
+                }
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                    for (int nb = 0; nb < SH::kNb; ++nb) {
+                        f32x4 c = {nref[nb], nref[nb], nref[nb], nref[nb]};
+#pragma unroll
+                        for (int dc = 0; dc < SH::kDc; ++dc) c = T::mfma16x16x32(kop[kk][dc], qop[nb][dc], c);
+                        sc[h][nb][kk] = c;
+                        __builtin_amdgcn_sched_barrier(0);  // keep the chain contiguous
+                    }
+            }
+            __builtin_amdgcn_s_setprio(0);
+        };
+        // O^T += V^T P^T of a tile (V stage st), and the row sums.
+        auto pv_product = [&](int st) __attribute__((always_inline)) {
+            typedef __attribute__((address_space(3))) uint8_t lds_u8;
+            lds_u8* vbase = (lds_u8*)&sm_v[st][0];
+            auto vread = [&](int dt, u32x4 (&vop)[SH::kHalves]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int h = 0; h < SH::kHalves; ++h) {
+                    const s16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(vbase + 32 * h * SH::kRowBytes + voff[dt]));
+                    const s16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_s16x4*)(vbase + (32 * h + 16) * SH::kRowBytes + voff[dt]));
+                    const u32x2 w0 = __builtin_bit_cast(u32x2, t0);
+                    const u32x2 w1 = __builtin_bit_cast(u32x2, t1);
+                    vop[h] = u32x4{w0[0], w0[1], w1[0], w1[1]};
+                }
+            };
+            __builtin_amdgcn_s_setprio(1);
+            u32x4 vcur[SH::kHalves], vnext[SH::kHalves];
+            vread(0, vcur);
+#pragma unroll
+            for (int dt = 0; dt < SH::kDt; ++dt) {
+                if (dt + 1 < SH::kDt) vread(dt + 1, vnext);
+#pragma unroll
+                for (int nb = 0; nb < SH::kNb; ++nb) {
+#pragma unroll
+                    for (int h = 0; h < SH::kHalves; ++h) o[nb][dt] = T::mfma16x16x32(vcur[h], pops[h][nb], o[nb][dt]);
+                    __builtin_amdgcn_sched_barrier(0);  // keep the products back to back
+                }
+#pragma unroll
+                for (int h = 0; h < SH::kHalves; ++h) vcur[h] = vnext[h];
+            }
+#pragma unroll
+            for (int nb = 0; nb < SH::kNb; ++nb) {
+#pragma unroll
+                for (int h = 0; h < SH::kHalves; ++h) osum[nb] = T::mfma16x16x32(ones, pops[h][nb], osum[nb]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __builtin_amdgcn_s_setprio(0);
+        };
+        // Probabilities of a tile whose S^T is in sc (K stage st): masked and
+        // biased first unless every key is present and visible to every row
+        // of the wave.  p = 2^sc; the exact step (row maxima, rescale of what
+        // is accumulated, new probabilities) runs when a row sees its first
+        // key or some probability exceeds 2^8 (inf and NaN included: as bit
+        // patterns of non-negative floats they order above 256).
+        auto softmax_tile = [&](int tile, int st) __attribute__((always_inline)) {
+            const int tile0 = tile * SH::kKeys;
+            const bool full = ((full_stages >> st) & 1u) != 0;
+            const bool fast = full && tile0 + SH::kKeys - 1 <= wave_first;
+            const float* smb = &sm_b[st][0];
+            if (!fast) {
+#pragma unroll
+                for (int h = 0; h < SH::kHalves; ++h)
+#pragma unroll
+                    for (int nb = 0; nb < SH::kNb; ++nb) {
+                        const int lim = pos[nb] - tile0 - 32 * h - 4 * lg;  // key (16*kk + j) must be <= lim
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk) {
+                            const f32x4 bias = full ? f32x4{0.f, 0.f, 0.f, 0.f}
+                                                    : *reinterpret_cast<const f32x4*>(&smb[32 * h + 16 * kk + 4 * lg]);
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                sc[h][nb][kk][j] = 16 * kk + j > lim ? kNegInf : sc[h][nb][kk][j] + bias[j];
+                        }
+                    }
+            }
+            bool need = false;
+#pragma unroll
+            for (int nb = 0; nb < SH::kNb; ++nb) need = need | ((m_run[nb] == kNegInf) & (pos[nb] >= tile0));
+#pragma unroll
+            for (int h = 0; h < SH::kHalves; ++h)
+#pragma unroll
+                for (int nb = 0; nb < SH::kNb; ++nb) {
+                    float p[8];
+                    uint32_t top = 0;
+#pragma unroll
+                    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            p[4 * kk + j] = fast_exp2(sc[h][nb][kk][j]);
+                            top = max(top, __float_as_uint(p[4 * kk + j]));
+                        }
+                    need = need | (top > __float_as_uint(kPSumLimit));
+                    pops[h][nb] = u32x4{T::pack(p[0], p[1]), T::pack(p[2], p[3]), T::pack(p[4], p[5]), T::pack(p[6], p[7])};
+                }
+            if (__builtin_amdgcn_ballot_w64(need)) {
+#pragma unroll
+                for (int nb = 0; nb < SH::kNb; ++nb) {
+                    float r = kNegInf;
+#pragma unroll
+                    for (int h = 0; h < SH::kHalves; ++h)
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) r = fmaxf(r, sc[h][nb][kk][j] - nref[nb]);
+                    const float mn = fmaxf(m_run[nb], row4_max(r));
+                    const float alpha = (m_run[nb] == kNegInf || mn == kNegInf) ? 1.f : fast_exp2(m_run[nb] - mn);
+                    const float shift = mn == kNegInf ? 0.f : nref[nb] + mn;
+                    m_run[nb] = mn;
+                    nref[nb] = mn == kNegInf ? 0.f : -mn;
+                    osum[nb] *= alpha;
+#pragma unroll
+                    for (int dt = 0; dt < SH::kDt; ++dt) o[nb][dt] *= alpha;
+#pragma unroll
+                    for (int h = 0; h < SH::kHalves; ++h) {
+                        float p[8];
+#pragma unroll
+                        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) p[4 * kk + j] = fast_exp2(sc[h][nb][kk][j] - shift);
+                        pops[h][nb] =
+                            u32x4{T::pack(p[0], p[1]), T::pack(p[2], p[3]), T::pack(p[4], p[5]), T::pack(p[6], p[7])};
+                    }
+                }
+            }
+        };
+
+        // Step i: S^T of tile i+1, O^T += V^T P^T of tile i (step 0: done
+        // in the prologue), then the probabilities of tile i+1 (products
+        // skipped for tiles past the wave's last visible key).
+        auto step = [&](int i, bool pv) __attribute__((always_inline)) {
+            const int tile = t_begin + i;
+            const bool next_vis = i + 1 < ntiles && (tile + 1) * SH::kKeys <= wave_last;
+            if (next_vis) s_product((i + 1) & (kPfStages - 1));
+            if (pv && tile * SH::kKeys <= wave_last) pv_product(i & (kPfStages - 1));
+            if (next_vis) softmax_tile(tile + 1, (i + 1) & (kPfStages - 1));
+        };
+
+        if (ntiles > 0) {
+            // Prologue: K and V of tile 0 (its page by a scalar lookup: the
+            // window's vector load is first needed after the barrier) land
+            // with the queries; tile 0 is then computed whole while K of
+            // tiles 1, 2 and V of tile 1 are in flight.
+            const int key0 = t_begin * SH::kKeys;
+            const int64_t page0 = ctable[key0 >> bs_shift];
+            const bool whole0 = key0 + SH::kKeys <= chunk_end && page0 >= 0 && page0 < a.num_blocks;
+            const int64_t off0 =
+                whole0 ? page0 * page_bytes_g + (int64_t)(key0 & (a.block_size - 1)) * row_bytes_g : (int64_t)-1;
+            issue_k(t_begin, 0, off0);
+            issue_v(t_begin, 0, off0);
+            if (t_begin + kWave < t_end) next_pages = window_pages(t_begin + kWave);
+            landed_barrier();
+            tile_offs = window_offsets(tile_pages, tile_base);
+            int64_t pend = -1;  // offset of the last K tile issued, whose V is still to come
+            if (ntiles > 1) {  // tiles 1 and 2 lie in the first window
+                const int64_t off1 = lane_value(tile_offs, 1);
+                issue_k(t_begin + 1, 1, off1);
+                if (ntiles > 2) {
+                    pend = lane_value(tile_offs, 2);
+                    issue_k(t_begin + 2, 2, pend);
+                }
+                issue_v(t_begin + 1, 1, off1);
+            }
+            // Queries scaled by scale*log2(e) (they landed at the barrier).
+#pragma unroll
+            for (int nb = 0; nb < SH::kNb; ++nb)
+#pragma unroll
+                for (int dc = 0; dc < SH::kDc; ++dc)
+#pragma unroll
+                    for (int w = 0; w < 4; ++w)
+                        qop[nb][dc][w] = T::pack(T::lo(qop[nb][dc][w]) * a.scale_log2, T::hi(qop[nb][dc][w]) * a.scale_log2);
+            if (key0 <= wave_last) {
+                s_product(0);
+                softmax_tile(t_begin, 0);
+                pv_product(0);
+            }
+            // Pairs of steps (i0, i0+1), i0 even: barrier B publishes K of
+            // i0+1, i0+2 and V of i0, i0+1; then the copies of K i0+3, i0+4
+            // and V i0+2, i0+3 go out (their stages were last read before B).
+            for (int i0 = 0; i0 < ntiles; i0 += 2) {
+                landed_barrier();
+                if (i0 + 2 < ntiles) {
+                    int64_t off3 = -1, off4 = -1;
+                    if (i0 + 3 < ntiles) {
+                        const int t3 = t_begin + i0 + 3, last = i0 + 4 < ntiles ? t3 + 1 : t3;
+                        const int base0 = tile_base;
+                        if (t3 < base0 + kWave) off3 = lane_value(tile_offs, t3 - base0);
+                        if (last >= base0 + kWave) next_window();
+                        if (t3 >= base0 + kWave) off3 = lane_value(tile_offs, t3 - tile_base);
+                        if (i0 + 4 < ntiles) off4 = lane_value(tile_offs, t3 + 1 - tile_base);
+                        issue_k(t3, (i0 + 3) & (kPfStages - 1), off3);
+                    }
+                    if (i0 + 4 < ntiles) issue_k(t_begin + i0 + 4, (i0 + 4) & (kPfStages - 1), off4);
+                    issue_v(t_begin + i0 + 2, (i0 + 2) & (kPfStages - 1), pend);
+                    if (i0 + 3 < ntiles) issue_v(t_begin + i0 + 3, (i0 + 3) & (kPfStages - 1), off3);
+                    pend = off4;
+                }
+                step(i0, i0 > 0);
+                if (i0 + 1 < ntiles) step(i0 + 1, true);
+            }
+        }
+    } else {
     // Prologue: only the first tile in flight, so the first products wait
     // for the queries and one tile; the pairs that follow are (t, t+1) with
     // t - t_begin odd, each issued one pair ahead.
@@ -988,12 +1292,14 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             }
         }
     }
+    }  // old loop
     // Drain the trailing copies before the work-group's LDS can be reassigned.
     wait_vmcnt_all();
 
 #pragma unroll
     for (int nb = 0; nb < SH::kNb; ++nb) {
-        const float l_row = row4_sum(l_part[nb]);
+        // The pipelined loop's sums come from the matrix core, whole per lane.
+        const float l_row = PIPE ? osum[nb][0] : row4_sum(l_part[nb]);
         if (qi[nb] >= qlen) continue;
         const int64_t rowid = (row0 + qi[nb]) * a.q_heads + head[nb];
         if (nchunks == 1) {

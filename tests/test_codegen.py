@@ -53,7 +53,11 @@ def stray_waits(ins):
     for i, s in enumerate(ins):
         if s.startswith("global_load_lds"):
             copies = True
-        if s.startswith("s_barrier"):
+        if s.startswith("s_endpgm"):
+            # Execution does not fall through: the instructions laid out
+            # next belong to blocks reached by branches from elsewhere.
+            armed, pending = False, None
+        elif s.startswith("s_barrier"):
             armed, pending = True, None
         elif s.startswith("s_waitcnt") and "vmcnt(0)" in s:
             if armed and copies and not (i + 1 < len(ins) and ins[i + 1].startswith("s_barrier")):
@@ -85,3 +89,7 @@ def test_stray_wait_detector_flags_a_planted_wait():
     # A full wait before any copy of the barrier's interval is issued is harmless.
     early = clean[:2] + ["s_waitcnt vmcnt(0)"] + clean[2:]
     assert stray_waits(early) == []
+    # So is the drain before a work-group ends: the product laid out after
+    # s_endpgm is not executed next.
+    ending = clean[:3] + ["s_waitcnt vmcnt(0)", "s_endpgm"] + clean[4:]
+    assert stray_waits(ending) == []

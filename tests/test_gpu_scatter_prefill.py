@@ -259,6 +259,27 @@ def _two_sequence_case(head_dim, heads, kv_heads, block, dtype, seed):
     return [q, kc, vc, cu, starts, tables, lens]
 
 
+@pytest.mark.parametrize("dtype,chunk_tokens,priors", [
+    (torch.bfloat16, 8192, [6000, 4500]),  # one chunk per sequence: items of 96 and 73 tiles
+    (torch.float16, 4160, [6000, 4500]),   # first chunks of 65 tiles, a second chunk each
+    (torch.bfloat16, 4224, [4100, 130]),   # 66 tiles, the last one partial
+])
+def test_prefill_items_longer_than_a_page_window(dtype, chunk_tokens, priors):
+    """Items of more than 64 key tiles: the tile loop moves to its next window
+    of page offsets (64 tiles, loaded a window ahead) inside the item."""
+    case = workloads.chunked_prefill_case(device=DEV, num_seqs=2, new_tokens=96, block_size=256, dtype=dtype,
+                                          priors=priors, seed=chunk_tokens)
+    write_kv_cache_slots(case["key_cache"], case["value_cache"], case["slot_mapping"], case["new_key"],
+                         case["new_value"], backend="hip")
+    names = ("q", "key_cache", "value_cache", "cu_seqlens_q", "query_starts", "block_tables", "context_lens")
+    args = [case[n] for n in names]
+    print(f"prefill long items {dtype} chunk={chunk_tokens} priors={priors}", flush=True)
+    actual = paged_prefill_attention(*args, 256, backend="hip", chunk_tokens=chunk_tokens)
+    cpu_args = [a.cpu() for a in args]
+    assert max_err(actual, paged_oracle.paged_prefill_attention(*cpu_args, 256, cast=False)) <= GATE[dtype]
+    assert max_err(actual, c_oracle.paged_prefill(*cpu_args, 256)) <= GATE[dtype]
+
+
 @pytest.mark.parametrize("head_dim,block,chunk_tokens,dtype,heads,kv_heads", [
     (64, 256, 0, torch.bfloat16, 16, 8), (64, 256, 256, torch.float16, 16, 8), (8, 256, 0, torch.bfloat16, 8, 1),
     (16, 16, 0, torch.float16, 4, 4), (40, 5, 0, torch.bfloat16, 16, 4), (72, 64, 192, torch.float16, 9, 3),
