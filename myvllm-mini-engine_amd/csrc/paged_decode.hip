@@ -116,11 +116,24 @@ int decode_tile_tokens(int64_t head_dim) {
 constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 
 // Host-side plan (lengths stay on the device, so it depends on the table
-// capacity only).  Enough (sequence, kv head) units to occupy every CU, or a
-// short capacity: one work-group per unit over the whole context, merged in
-// LDS.  Otherwise split-K into partitions of 4-wave work-groups, sized to
-// give every CU about four work-groups, plus a merge kernel.  `requested` > 0
-// forces split-K with that partition length (rounded to the wave tiling).
+// capacity only).  Enough (sequence, kv head) units to occupy every CU, a
+// capacity of one 16-wave step, or two steps with more than a quarter of the
+// CUs' worth of units: one work-group per unit over the whole context, merged
+// in LDS.  Otherwise split-K into partitions of 4-wave work-groups, sized to
+// give every CU about two work-groups (at least one 4-wave step each), plus
+// a merge kernel.  `requested` > 0 forces split-K with that partition length
+// (rounded to the wave tiling).
+//
+// Measured at head_dim 128 (bf16, block 16, 16/8 heads, µs per call in a
+// graph): whole-sequence against split-K at 64/128/256 keys.
+// * ctx 128: whole 4.9-5.1, any split about 2 µs more (the merge launch).
+// * ctx 256: level up to 64 units; whole ahead from 128 units.
+// * ctx 512: split at 64 ahead up to 64 units (1 unit 7.96 -> 6.87, 64 units
+//   8.18 -> 7.82); whole ahead from 128 units (128 units 9.01 vs 9.98).
+// * ctx 1024-4096 with 8-64 units: the best partition gives about 512
+//   work-groups (1024 keys x 8 units: 256-key parts 9.69, 64-key 7.30; 1024
+//   x 64: 11.61 -> 9.93 at 128; 2048 x 32: 11.56 -> 10.48 at 128); the
+//   earlier plan took at least 256 keys for a target of 1024 work-groups.
 DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                             int64_t block_size, int64_t table_width, int64_t requested) {
     DecodePlan p{};
@@ -132,11 +145,9 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     const int64_t split_step = tile * kSplitWaves;
     const int64_t whole_step = tile * kWholeWaves;
     int64_t part;
-    if (requested <= 0 && (units >= kDeviceCUs - kDeviceCUs / 16 || cap <= 2 * whole_step)) {
-        // Whole-sequence work-groups; also when the capacity is at most two
-        // 16-wave steps (launch- and latency-bound, a merge would only add a
-        // launch).  Longer contexts with few units split instead, so that a
-        // few work-groups do not each walk a long context alone.
+    const bool whole = units >= kDeviceCUs - kDeviceCUs / 16 || cap <= whole_step ||
+                       (cap <= 2 * whole_step && units > kDeviceCUs / 4);
+    if (requested <= 0 && whole) {
         p.waves = cap >= 2 * whole_step ? kWholeWaves : kSplitWaves;
         part = (cap + tile - 1) / tile * tile;
     } else {
@@ -144,9 +155,8 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
         if (requested > 0) {
             part = requested;
         } else {
-            constexpr int64_t kTargetGroups = 4 * kDeviceCUs;
+            constexpr int64_t kTargetGroups = 2 * kDeviceCUs;
             part = (cap * units + kTargetGroups - 1) / kTargetGroups;
-            if (part < 256) part = 256;  // short partitions only add merge traffic
         }
         part = (part + split_step - 1) / split_step * split_step;
         const int64_t cap_steps = (cap + split_step - 1) / split_step * split_step;
