@@ -12,6 +12,13 @@ host instead of walking positions one by one:
 * no slot is written twice, and no page written by one request may appear in
   another request's table (shared prefix pages are read-only).
 
+``validate`` re-checks the batch at the model's execution boundary, as the
+reference's ``PrefillBatch.validate`` does (batch.py:139-162): the cache
+geometry, the tensors' type, device and layout, a fingerprint of every
+tensor taken at construction (storage pointer, version counter, shape,
+strides, dtype, device -- an in-place edit or a swapped tensor is refused
+without reading the device), the model's context limit and vocabulary.
+
 The checks run in three stages — argument types, the per-request layout
 (each rule over the whole batch at once), then the rules that relate
 requests (duplicate slots, written pages that another request reads) — and
@@ -24,7 +31,7 @@ message.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from numbers import Integral
 
 import torch
@@ -96,6 +103,16 @@ def _check_shared_writes(table: torch.Tensor, pages_per_row: torch.Tensor, slots
         raise ValueError("prefill cannot write a physical page shared by requests")
 
 
+def _fingerprint(tensor: torch.Tensor) -> tuple:
+    """What an in-place edit or a swapped tensor changes, read on the host."""
+    return (tensor.data_ptr(), tensor._version, tuple(tensor.shape), tuple(tensor.stride()), tensor.dtype,
+            tensor.device)
+
+
+_TENSOR_FIELDS = ("input_ids", "positions", "slot_mapping", "cu_seqlens_q", "query_starts", "context_lens",
+                  "block_tables")
+
+
 @dataclass(frozen=True)
 class PrefillBatch:
     input_ids: torch.Tensor
@@ -111,6 +128,10 @@ class PrefillBatch:
     block_ids: tuple
     block_size: int
     num_blocks: int
+    # Host copies taken at construction: the largest token id, and one
+    # fingerprint per tensor (empty when the batch was built by hand).
+    max_token_id: int = field(default=-1, repr=False)
+    fingerprints: tuple = field(default=(), repr=False, compare=False)
 
     @property
     def batch_size(self):
@@ -173,7 +194,30 @@ class PrefillBatch:
 
         width = int(pages_per_row.max())
         clean = tuple(tuple(row[:int(n)]) for row, n in zip(rows, pages_per_row))
-        on_device = [t.to(device) for t in (token_ids, positions, slots, offsets, start, ends,
-                                           table[:, :width].contiguous())]
+        # Outside inference mode the device tensors keep version counters, so
+        # validate() can see in-place edits without a device-to-host copy.
+        with torch.inference_mode(False):
+            on_device = [t.to(device).clone() for t in (token_ids, positions, slots, offsets, start, ends,
+                                                        table[:, :width].contiguous())]
         return cls(*on_device, tuple(lengths.tolist()), tuple(offsets.tolist()), tuple(starts), clean,
-                   block_size, num_blocks)
+                   block_size, num_blocks, int(token_ids.max()), tuple(_fingerprint(t) for t in on_device))
+
+    def validate(self, *, block_size, num_blocks, device, max_position_embeddings, vocab_size):
+        """The execution-boundary checks of the reference (batch.py:139-162):
+        after them the scatter and prefill kernels may run with
+        validate=False.  Reads host state only."""
+        if self.block_size != block_size or self.num_blocks != num_blocks:
+            raise ValueError("prefill metadata does not match KV cache geometry")
+        tensors = [getattr(self, name) for name in _TENSOR_FIELDS]
+        if len(self.fingerprints) != len(tensors):
+            raise ValueError("construct prefill metadata with PrefillBatch.from_sequences")
+        device = torch.device(device)
+        if not all(isinstance(t, torch.Tensor) and t.dtype == torch.int64 and t.device == device
+                   and t.is_contiguous() for t in tensors):
+            raise ValueError("prefill metadata must be contiguous int64 tensors on the cache device")
+        if tuple(_fingerprint(t) for t in tensors) != self.fingerprints:
+            raise ValueError("prefill metadata was modified; rebuild it with from_sequences")
+        if max(s + n for s, n in zip(self.starts, self.query_lengths)) > max_position_embeddings:
+            raise ValueError("prefill query range exceeds model context limit")
+        if self.max_token_id >= vocab_size:
+            raise ValueError("prefill token ID exceeds model vocabulary")

@@ -6,6 +6,8 @@ same ValueError messages fire before any kernel could run, and CPU tensors
 are refused by the hip backend instead of being computed on the CPU.
 """
 
+import dataclasses
+
 import pytest
 import torch
 
@@ -188,6 +190,43 @@ def test_prefill_metadata_positions_slots_and_readonly_prefix_sharing():
 def test_prefill_metadata_rejects_invalid_layout(sequences, tables, starts, error):
     with pytest.raises(ValueError, match=error):
         metadata(sequences, tables, starts)
+
+
+def test_prefill_metadata_validate_at_the_execution_boundary():
+    """PrefillBatch.validate (reference batch.py:139-162): geometry, tensor
+    type and device, in-place edits and swapped tensors, the context limit and
+    the vocabulary, each with the reference's message."""
+    batch = metadata([[5, 6, 7], [8, 9]], [[3, 1, -1], [3, 2]], [4, 4])
+    ok = dict(block_size=4, num_blocks=16, device="cpu", max_position_embeddings=7, vocab_size=10)
+    batch.validate(**ok)  # context 7 and token 9 are the largest allowed
+    for change, message in [
+        (dict(block_size=8), "geometry"), (dict(num_blocks=17), "geometry"),
+        (dict(max_position_embeddings=6), "context limit"), (dict(vocab_size=9), "vocabulary"),
+    ]:
+        with pytest.raises(ValueError, match=message):
+            batch.validate(**{**ok, **change})
+    # A tensor edited in place after construction (its version counter moves).
+    edited = metadata([[5, 6, 7], [8, 9]], [[3, 1, -1], [3, 2]], [4, 4])
+    edited.slot_mapping.add_(0)
+    with pytest.raises(ValueError, match="was modified"):
+        edited.validate(**ok)
+    # A tensor swapped for another with the same values.
+    swapped = dataclasses.replace(batch, context_lens=batch.context_lens.clone())
+    with pytest.raises(ValueError, match="was modified"):
+        swapped.validate(**ok)
+    # Wrong dtype or layout of a metadata tensor.
+    as_int32 = dataclasses.replace(batch, positions=batch.positions.int())
+    with pytest.raises(ValueError, match="contiguous int64"):
+        as_int32.validate(**ok)
+    # Built by hand rather than by from_sequences: no fingerprints.
+    fields = {f.name: getattr(batch, f.name) for f in dataclasses.fields(batch)
+              if f.name not in ("max_token_id", "fingerprints")}
+    with pytest.raises(ValueError, match="from_sequences"):
+        PrefillBatch(**fields).validate(**ok)
+    # Construction under inference mode still keeps version counters.
+    with torch.inference_mode():
+        inferred = metadata([[5, 6, 7], [8, 9]], [[3, 1, -1], [3, 2]], [4, 4])
+    inferred.validate(**ok)
 
 
 @pytest.mark.parametrize("starts,block_size,error", [
