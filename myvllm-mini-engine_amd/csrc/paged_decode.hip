@@ -93,7 +93,7 @@ struct DecodePlan {
     int partition;
     int max_parts;
     int gtile;  // G of the kernel instance
-    int waves;  // waves per work-group (kSplitWaves or kWholeWaves)
+    int waves;  // waves per work-group (kSplitWaves, kWholeWaves or kLongWaves)
     bool stream;  // non-temporal K/V loads
 };
 
@@ -119,7 +119,7 @@ constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 // capacity only).  Enough (sequence, kv head) units to occupy every CU, a
 // capacity of one 16-wave step, or two steps with more than a quarter of the
 // CUs' worth of units: one work-group per unit over the whole context, merged
-// in LDS.  Otherwise split-K into partitions of 4-wave work-groups, sized to
+// in LDS (8 waves, 16 for units of at least kLongUnitBytes).  Otherwise split-K into partitions of 4-wave work-groups, sized to
 // give every CU about two work-groups (at least one 4-wave step each), plus
 // a merge kernel.  `requested` > 0 forces split-K with that partition length
 // (rounded to the wave tiling).
@@ -143,12 +143,12 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     const int64_t cap = table_width * block_size;
     const int64_t units = batch * kv_heads * (group / p.gtile);
     const int64_t split_step = tile * kSplitWaves;
-    const int64_t whole_step = tile * kWholeWaves;
+    const int64_t whole_step = tile * 16;  // the capacity unit the thresholds below were measured in
     int64_t part;
     const bool whole = units >= kDeviceCUs - kDeviceCUs / 16 || cap <= whole_step ||
                        (cap <= 2 * whole_step && units > kDeviceCUs / 4);
     if (requested <= 0 && whole) {
-        p.waves = cap >= 2 * whole_step ? kWholeWaves : kSplitWaves;
+        p.waves = cap < 2 * whole_step ? kSplitWaves : cap * head_dim * 4 >= kLongUnitBytes ? kLongWaves : kWholeWaves;
         part = (cap + tile - 1) / tile * tile;
     } else {
         p.waves = kSplitWaves;
@@ -193,7 +193,8 @@ void launch_decode_nw(const DecodeArgs& a, int units, bool page_uniform, bool st
 
 template <typename T, int D, int G>
 void launch_decode(const DecodeArgs& a, const DecodePlan& p, int units, bool page_uniform, hipStream_t s) {
-    if (p.waves == kWholeWaves) launch_decode_nw<T, D, G, kWholeWaves>(a, units, page_uniform, p.stream, s);
+    if (p.waves == kLongWaves) launch_decode_nw<T, D, G, kLongWaves>(a, units, page_uniform, p.stream, s);
+    else if (p.waves == kWholeWaves) launch_decode_nw<T, D, G, kWholeWaves>(a, units, page_uniform, p.stream, s);
     else launch_decode_nw<T, D, G, kSplitWaves>(a, units, page_uniform, p.stream, s);
     if (a.max_parts > 1)
         hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(units / a.kv_heads / a.gtiles * a.q_heads),

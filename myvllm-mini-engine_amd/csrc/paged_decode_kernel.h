@@ -38,7 +38,17 @@
 namespace mvme {
 
 constexpr int kSplitWaves = 4;   // waves per work-group in split-K mode
-constexpr int kWholeWaves = 16;  // waves per work-group covering a whole sequence
+// Waves per work-group covering a whole sequence: 8, or 16 when one unit's
+// capacity holds kLongUnitBytes of K+V or more.  Uniform decode at head_dim
+// 128 (fp16, block 256, us per call): B32/ctx2048 43.7 at 16 waves, 42.9 at
+// 8 (45.2 at 12); B128/ctx1024 91.4 -> 83.9; B64/ctx2048 83.8 -> 83.3; but
+// B32/ctx4096 84.4 -> 85.3, and the ragged B64 case (contexts up to 4096,
+// block 16) 86.6 -> 91.1, where the longest units' work-groups finish last
+// and stream faster with more waves in flight.  A plain streaming read of a
+// 256 MiB layer likewise peaks at 8 waves per CU (6.8 TB/s; 16 waves 6.4).
+constexpr int kWholeWaves = 8;
+constexpr int kLongWaves = 16;
+constexpr int64_t kLongUnitBytes = int64_t(2) << 20;
 constexpr int kLptMax = 256;     // largest batch whose units go longest context first
 static_assert(kSplitWaves * kWave >= kLptMax, "one thread per sequence key");
 constexpr int kDecodeLoads = 4;  // K (and V) loads per lane per iteration
