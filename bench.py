@@ -946,7 +946,7 @@ def main(argv=None):
                    "algorithmic_bytes_per_call": layer_bytes(), "timing": "hipGraph of 28 calls per step"},
         "roofline": {"bound": "hbm", "achieved": achieved_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved_gbs / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel": "paged_decode_kernel (fp16, D=128, G=2, 16 waves)"},
+                     "kernel": "paged_decode_kernel (fp16, D=128, G=2, 8 waves)"},
         "parity": parity,
         "reference_published": {"us_per_call_rtx5080": REFERENCE_US_PER_CALL,
                                 "speedup_vs_rtx5080": REFERENCE_US_PER_CALL / (per_call_ms * 1e3)},
