@@ -197,16 +197,17 @@ def test_mfma_prefill_ragged_priors(dtype, priors, block_size):
     assert max_err(actual, c_oracle.paged_prefill(*cpu, block_size)) <= GATE[dtype]
 
 
+@pytest.mark.parametrize("block", [16, 64])  # per-row copies; whole-tile pages (the pipelined loop)
 @pytest.mark.parametrize("group,heads", [(1, 8), (4, 16), (8, 16)])
-def test_mfma_prefill_gqa_groups(group, heads):
+def test_mfma_prefill_gqa_groups(group, heads, block):
     dtype = torch.bfloat16
     gen = torch.Generator().manual_seed(group)
     kv_heads = heads // group
-    block = 16
-    pages = 24
+    width = -(-140 // block)
+    pages = 2 * width + 4
     kc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
     vc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
-    tables = torch.randperm(pages, generator=gen)[:20].view(2, 10)
+    tables = torch.randperm(pages, generator=gen)[:2 * width].view(2, width)
     cu = torch.tensor([0, 50, 71])
     starts = torch.tensor([90, 3])
     lens = starts + (cu[1:] - cu[:-1])
@@ -217,11 +218,12 @@ def test_mfma_prefill_gqa_groups(group, heads):
     assert max_err(actual, expected) <= GATE[dtype]
 
 
+@pytest.mark.parametrize("block", [16, 256])  # per-row copies; whole-tile pages (the pipelined loop)
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("group,heads,chunk_tokens", [
     (3, 24, 0), (5, 40, 256), (7, 28, 0), (7, 28, 192), (6, 12, 320), (40, 40, 0), (100, 100, 256),
 ])
-def test_mfma_prefill_groups_not_dividing_the_row_block(dtype, group, heads, chunk_tokens):
+def test_mfma_prefill_groups_not_dividing_the_row_block(dtype, group, heads, chunk_tokens, block):
     """Groups that do not divide the 256 rows of a query block (Qwen-family
     layouts such as 28/4 and 40/8 heads): the block holds 256 // group tokens
     and its last 256 % group rows are idle.  Every head of every token is
@@ -229,7 +231,8 @@ def test_mfma_prefill_groups_not_dividing_the_row_block(dtype, group, heads, chu
     fail, with and without a key split (the merge then reads the partials)."""
     gen = torch.Generator().manual_seed(1000 + group)
     kv_heads = heads // group
-    block, pages, width = 16, 200, 90
+    width = -(-1440 // block)
+    pages = 2 * width + 20
     kc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
     vc = torch.randn(pages, block, kv_heads, 128, generator=gen).to(dtype)
     tables = torch.randperm(pages, generator=gen)[:2 * width].view(2, width)
@@ -238,7 +241,7 @@ def test_mfma_prefill_groups_not_dividing_the_row_block(dtype, group, heads, chu
     lens = starts + (cu[1:] - cu[:-1])
     q = torch.randn(227, heads, 128, generator=gen).to(dtype)
     args = [q, kc, vc, cu, starts, tables, lens]
-    print(f"prefill group={group} heads={heads} chunk={chunk_tokens} {dtype}", flush=True)
+    print(f"prefill group={group} heads={heads} chunk={chunk_tokens} block={block} {dtype}", flush=True)
     actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip", chunk_tokens=chunk_tokens)
     expected = paged_oracle.paged_prefill_attention(*args, block, cast=False)
     assert max_err(actual, expected) <= GATE[dtype]
@@ -406,16 +409,19 @@ def test_prefill_walk_over_more_than_64_sequences(chunk_tokens):
     assert max_err(actual, expected) <= GATE[dtype]
 
 
-def test_trusted_mode_offsets_out_of_order_stay_in_bounds():
+@pytest.mark.parametrize("block", [16, 64])
+def test_trusted_mode_offsets_out_of_order_stay_in_bounds(block):
     """validate=False with query offsets that are not monotone or pass the
     packed rows: the kernel clamps them to the rows, so it neither writes
     past the output nor loops over absurd block counts; rows no sequence
     covers are unspecified, every value finite."""
-    dtype, block = torch.bfloat16, 16
+    dtype = torch.bfloat16
     gen = torch.Generator().manual_seed(5)
-    kc = torch.randn(40, block, 8, 128, generator=gen).to(dtype).to(DEV)
-    vc = torch.randn(40, block, 8, 128, generator=gen).to(dtype).to(DEV)
-    tables = torch.randperm(40, generator=gen)[:36].view(3, 12).to(DEV)
+    width = -(-192 // block)
+    pages = 3 * width + 4
+    kc = torch.randn(pages, block, 8, 128, generator=gen).to(dtype).to(DEV)
+    vc = torch.randn(pages, block, 8, 128, generator=gen).to(dtype).to(DEV)
+    tables = torch.randperm(pages, generator=gen)[:3 * width].view(3, width).to(DEV)
     q = torch.randn(71, 16, 128, generator=gen).to(dtype).to(DEV)
     starts = torch.tensor([90, 3, 10], device=DEV)
     lens = torch.tensor([140, 50, 100], device=DEV)
