@@ -1572,85 +1572,129 @@ __global__ __launch_bounds__(kPfThreads, 1) void paged_prefill_mfma_kernel(Prefi
 // head_dim.
 constexpr int kMergeThreads = 256;
 
+// One chunk's partial: 8 dims of the row (two 16-byte words for fp32
+// partials, one for bf16) and its (reference, sum) pair.
+template <typename T>
+struct MergePart {
+    u32x4 raw[2];
+    float2 ml;
+};
+
+template <typename T>
+__device__ inline MergePart<T> merge_load(const PrefillArgs& a, int64_t rowid, int d0, int c) {
+    using P = typename PartialOf<T>::type;
+    MergePart<T> part;
+    const int64_t slot = (int64_t)c * a.ws_rows + rowid;  // chunk c's slot: c * ws_rows + rowid
+    const u32x4* po = reinterpret_cast<const u32x4*>(static_cast<const P*>(a.ws_o) + slot * a.part_dim + d0);
+    part.raw[0] = po[0];
+    if constexpr (sizeof(P) == 4) part.raw[1] = po[1];
+    part.ml = reinterpret_cast<const float2*>(a.ws_ml)[slot];
+    return part;
+}
+
+// Folds G chunks into the running (reference, sum, acc); entries with
+// live = false get weight zero.  The reference moves (with a rescale) only
+// when the group holds a larger maximum.
+template <typename T, int G>
+__device__ inline void merge_absorb(const MergePart<T> (&parts)[G], const bool (&live)[G], float& mref, float& sum,
+                                    float (&acc)[8]) {
+    using P = typename PartialOf<T>::type;
+    float m[G];
+    float gmax = kNegInf;
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        m[k] = live[k] ? parts[k].ml.x : kNegInf;
+        gmax = fmaxf(gmax, m[k]);
+    }
+    if (gmax > mref) {
+        const float scale = mref == kNegInf ? 0.f : fast_exp2(mref - gmax);
+        sum *= scale;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] *= scale;
+        mref = gmax;
+    }
+    const float ref = mref == kNegInf ? 0.f : mref;
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        f32x4 x0, x1;
+        if constexpr (sizeof(P) == 4) {
+            x0 = __builtin_bit_cast(f32x4, parts[k].raw[0]);
+            x1 = __builtin_bit_cast(f32x4, parts[k].raw[1]);
+        } else {
+            const u32x4 w = parts[k].raw[0];
+            x0 = f32x4{T::lo(w[0]), T::hi(w[0]), T::lo(w[1]), T::hi(w[1])};
+            x1 = f32x4{T::lo(w[2]), T::hi(w[2]), T::lo(w[3]), T::hi(w[3])};
+        }
+        // Chunk weight: its probability sum at the common reference.
+        const float w = m[k] == kNegInf ? 0.f : parts[k].ml.y * fast_exp2(m[k] - ref);
+        sum += w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc[i] = fmaf(x0[i], w, acc[i]);
+            acc[4 + i] = fmaf(x1[i], w, acc[4 + i]);
+        }
+    }
+}
+
+// Chunks c0 .. c0+G-1 below nchunks, every load of the group in flight
+// together (loads guarded one by one, each followed by its use, would each
+// wait for the previous one): chunks past the last re-read the last one --
+// in bounds and cached -- and get weight zero.
+template <typename T, int G>
+__device__ inline void merge_group(const PrefillArgs& a, int64_t rowid, int d0, int c0, int nchunks, float& mref,
+                                   float& sum, float (&acc)[8]) {
+    MergePart<T> parts[G];
+    bool live[G];
+#pragma unroll
+    for (int k = 0; k < G; ++k) {
+        parts[k] = merge_load<T>(a, rowid, d0, min(c0 + k, nchunks - 1));
+        live[k] = c0 + k < nchunks;
+    }
+    merge_absorb<T, G>(parts, live, mref, sum, acc);
+}
+
+// Grid: (packed token, group of kMergeThreads (head, 8-dim) pairs).
 template <typename T>
 __global__ __launch_bounds__(kMergeThreads) void paged_prefill_merge_kernel(PrefillArgs a) {
     const int64_t token = blockIdx.x;
     // Every token of consistent metadata is written by its block's first
     // item; the clamp keeps reads inside the workspace for any other value.
-    const int nchunks = min(a.ws_tok[token], a.max_chunks);
-    if (nchunks <= 1) return;
-    constexpr int kGroup = 8;  // chunks whose partials are loaded together
+    // The count is a scalar load; the first two chunks' partials (every
+    // merged row has at least two, and the workspace holds at least two
+    // chunks whenever this kernel runs) are requested before it is used, so
+    // that the count and the data cost one memory round trip, not two.
+    const int counted = a.ws_tok[token];
     const int dgroups = a.head_dim / 8;
-    for (int idx = threadIdx.x; idx < a.q_heads * dgroups; idx += kMergeThreads) {
-        const int head = idx / dgroups;
-        const int d0 = 8 * (idx - head * dgroups);
-        const int64_t rowid = token * a.q_heads + head;  // chunk c's slot: c * ws_rows + rowid
-        const float2* ml = reinterpret_cast<const float2*>(a.ws_ml) + rowid;
-        // One pass: every load of a group of chunks is in flight together,
-        // and the running reference moves (with a rescale) only when a
-        // group holds a larger maximum.
-        float mref = kNegInf, sum = 0.f;
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int c0 = 0; c0 < nchunks; c0 += kGroup) {
-            using P = typename PartialOf<T>::type;
-            // Every load of the group is issued before any is used (loads
-            // guarded one by one, each followed by its use, would each wait
-            // for the previous one).  Chunks past the last re-read the last
-            // one -- in bounds and cached -- and get weight zero below.
-            u32x4 raw[kGroup][2];
-            float2 mlc[kGroup];
-#pragma unroll
-            for (int k = 0; k < kGroup; ++k) {
-                const int c = min(c0 + k, nchunks - 1);
-                const int64_t slot = (int64_t)c * a.ws_rows + rowid;
-                const u32x4* po = reinterpret_cast<const u32x4*>(static_cast<const P*>(a.ws_o) + slot * a.part_dim + d0);
-                raw[k][0] = po[0];
-                if constexpr (sizeof(P) == 4) raw[k][1] = po[1];
-                mlc[k] = ml[(int64_t)c * a.ws_rows];
-            }
-            f32x4 x[kGroup][2];
-#pragma unroll
-            for (int k = 0; k < kGroup; ++k) {
-                if (c0 + k >= nchunks) mlc[k] = float2{kNegInf, 0.f};
-                if constexpr (sizeof(P) == 4) {
-                    x[k][0] = __builtin_bit_cast(f32x4, raw[k][0]);
-                    x[k][1] = __builtin_bit_cast(f32x4, raw[k][1]);
-                } else {
-                    const u32x4 w = raw[k][0];
-                    x[k][0] = f32x4{T::lo(w[0]), T::hi(w[0]), T::lo(w[1]), T::hi(w[1])};
-                    x[k][1] = f32x4{T::lo(w[2]), T::hi(w[2]), T::lo(w[3]), T::hi(w[3])};
-                }
-            }
-            float gmax = kNegInf;
-#pragma unroll
-            for (int k = 0; k < kGroup; ++k) gmax = fmaxf(gmax, mlc[k].x);
-            if (gmax > mref) {
-                const float scale = mref == kNegInf ? 0.f : fast_exp2(mref - gmax);
-                sum *= scale;
-#pragma unroll
-                for (int i = 0; i < 8; ++i) acc[i] *= scale;
-                mref = gmax;
-            }
-            const float ref = mref == kNegInf ? 0.f : mref;
-#pragma unroll
-            for (int k = 0; k < kGroup; ++k) {
-                // Chunk weight: its probability sum at the common reference.
-                const float w = mlc[k].x == kNegInf ? 0.f : mlc[k].y * fast_exp2(mlc[k].x - ref);
-                sum += w;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    acc[i] = fmaf(x[k][0][i], w, acc[i]);
-                    acc[4 + i] = fmaf(x[k][1][i], w, acc[4 + i]);
-                }
-            }
+    const int idx = blockIdx.y * kMergeThreads + threadIdx.x;
+    if (idx >= a.q_heads * dgroups) return;
+    const int head = idx / dgroups;
+    const int d0 = 8 * (idx - head * dgroups);
+    const int64_t rowid = token * a.q_heads + head;
+    const MergePart<T> first[2] = {merge_load<T>(a, rowid, d0, 0), merge_load<T>(a, rowid, d0, 1)};
+    // Keeps the two loads above the count test (the compiler would
+    // otherwise move them below it, after the count's round trip).
+    asm volatile("" : : : "memory");
+    const int nchunks = min(counted, a.max_chunks);
+    if (nchunks <= 1) return;
+    float mref = kNegInf, sum = 0.f;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // The rest in one group of 4 or 8 when it fits (a group's re-reads of
+    // the last chunk cost cache bandwidth, not HBM traffic).
+    if (nchunks > 2) {
+        if (nchunks <= 6) {
+            merge_group<T, 4>(a, rowid, d0, 2, nchunks, mref, sum, acc);
+        } else {
+            for (int c0 = 2; c0 < nchunks; c0 += 8) merge_group<T, 8>(a, rowid, d0, c0, nchunks, mref, sum, acc);
         }
-        const float inv = sum > 0.f ? 1.f / sum : 0.f;
-        const u32x4 wv = {T::pack(acc[0] * inv, acc[1] * inv), T::pack(acc[2] * inv, acc[3] * inv),
-                          T::pack(acc[4] * inv, acc[5] * inv), T::pack(acc[6] * inv, acc[7] * inv)};
-        uint16_t* orow =
-            static_cast<uint16_t*>(a.out) + dense_seq(a, token) * a.o_seq + token * a.o_tok + head * a.o_head;
-        *reinterpret_cast<u32x4*>(orow + d0) = wv;
     }
+    const bool both[2] = {true, true};
+    merge_absorb<T, 2>(first, both, mref, sum, acc);
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;
+    const u32x4 wv = {T::pack(acc[0] * inv, acc[1] * inv), T::pack(acc[2] * inv, acc[3] * inv),
+                      T::pack(acc[4] * inv, acc[5] * inv), T::pack(acc[6] * inv, acc[7] * inv)};
+    uint16_t* orow =
+        static_cast<uint16_t*>(a.out) + dense_seq(a, token) * a.o_seq + token * a.o_tok + head * a.o_head;
+    *reinterpret_cast<u32x4*>(orow + d0) = wv;
 }
 
 // ---------------------------------------------------------------------------
@@ -1970,7 +2014,8 @@ int launch_prefill(PrefillArgs a, const PrefillPlan& p, int64_t total_tokens, in
         if (dtype == MVME_FP16) launch_type(Half{});
         else launch_type(BFloat16{});
         if (p.max_chunks > 1) {
-            const dim3 grid((unsigned)total_tokens);
+            const int64_t pairs = q_heads * (a.head_dim / 8);
+            const dim3 grid((unsigned)total_tokens, (unsigned)((pairs + kMergeThreads - 1) / kMergeThreads));
             if (dtype == MVME_FP16)
                 hipLaunchKernelGGL((paged_prefill_merge_kernel<Half>), grid, dim3(kMergeThreads), 0, s, a);
             else
