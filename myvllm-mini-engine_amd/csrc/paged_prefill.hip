@@ -471,8 +471,16 @@ __device__ inline bool find_item_lanes(const PrefillArgs& a, int chunk_len, int 
     it.ctx = lane_value(m.ctx, sel);
     it.chunk_len = chunk_len;
     // Query blocks from the last to the first (as find_item), 64 at a time:
-    // lane l takes the l-th block of the group.
+    // lane l takes the l-th block of the group.  A sequence of one query
+    // block (a short prefill chunk) has its chunks as its items.
     const int64_t nblocks = query_blocks(a, it.qlen);
+    if (nblocks == 1) {
+        it.q0 = 0;
+        it.chunk = rem;
+        it.kv_end = block_kv_end(a, it.start, it.ctx, it.qlen, 0);
+        it.nchunks = lane_value(cnt, sel);
+        return true;
+    }
     for (int64_t g0 = 0; g0 < nblocks; g0 += kWave) {
         const int64_t bi = nblocks - 1 - (g0 + lane);
         int64_t e = 0;
@@ -578,15 +586,19 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         }
     }
     // Wave maximum / minimum: the lanes of one MFMA row index li hold the
-    // same rows, so lanes 0..15 cover every row of the wave (readlane, no
-    // LDS round trips).
+    // same rows, so lanes 0..15 cover every row of the wave: a reduction
+    // inside one 16-lane DPP row (quad swaps, then the half-row and row
+    // mirrors), read from lane 0.
     {
         int hi = wave_last, lo = wave_first;
-#pragma unroll
-        for (int l = 0; l < 16; ++l) {
-            hi = max(hi, lane_value(wave_last, l));
-            lo = min(lo, lane_value(wave_first, l));
-        }
+        hi = max(hi, __builtin_amdgcn_update_dpp(0, hi, kDppQuadSwap1, 0xf, 0xf, false));
+        lo = min(lo, __builtin_amdgcn_update_dpp(0, lo, kDppQuadSwap1, 0xf, 0xf, false));
+        hi = max(hi, __builtin_amdgcn_update_dpp(0, hi, kDppQuadSwap2, 0xf, 0xf, false));
+        lo = min(lo, __builtin_amdgcn_update_dpp(0, lo, kDppQuadSwap2, 0xf, 0xf, false));
+        hi = max(hi, __builtin_amdgcn_update_dpp(0, hi, kDppRowHalfMirror, 0xf, 0xf, false));
+        lo = min(lo, __builtin_amdgcn_update_dpp(0, lo, kDppRowHalfMirror, 0xf, 0xf, false));
+        hi = max(hi, __builtin_amdgcn_update_dpp(0, hi, kDppRowMirror, 0xf, 0xf, false));
+        lo = min(lo, __builtin_amdgcn_update_dpp(0, lo, kDppRowMirror, 0xf, 0xf, false));
         wave_last = __builtin_amdgcn_readfirstlane(hi);
         wave_first = __builtin_amdgcn_readfirstlane(lo);
     }
@@ -922,8 +934,10 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         // of the wave.  p = 2^sc; the exact step (row maxima, rescale of what
         // is accumulated, new probabilities) runs when a row sees its first
         // key or some probability exceeds 2^8 (inf and NaN included: as bit
-        // patterns of non-negative floats they order above 256).
-        auto softmax_tile = [&](int tile, int st) __attribute__((always_inline)) {
+        // patterns of non-negative floats they order above 256).  `first`:
+        // the item's first tile, where nothing is accumulated yet (every
+        // rescale factor is 1, so the rescale is skipped).
+        auto softmax_tile = [&](int tile, int st, bool first) __attribute__((always_inline)) {
             const int tile0 = tile * SH::kKeys;
             const bool full = ((full_stages >> st) & 1u) != 0;
             const bool fast = full && tile0 + SH::kKeys - 1 <= wave_first;
@@ -978,9 +992,11 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     const float shift = mn == kNegInf ? 0.f : nref[nb] + mn;
                     m_run[nb] = mn;
                     nref[nb] = mn == kNegInf ? 0.f : -mn;
-                    osum[nb] *= alpha;
+                    if (!first) {
+                        osum[nb] *= alpha;
 #pragma unroll
-                    for (int dt = 0; dt < SH::kDt; ++dt) o[nb][dt] *= alpha;
+                        for (int dt = 0; dt < SH::kDt; ++dt) o[nb][dt] *= alpha;
+                    }
 #pragma unroll
                     for (int h = 0; h < SH::kHalves; ++h) {
                         float p[8];
@@ -1003,7 +1019,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             const bool next_vis = i + 1 < ntiles && (tile + 1) * SH::kKeys <= wave_last;
             if (next_vis) s_product((i + 1) & (kPfStages - 1));
             if (pv && tile * SH::kKeys <= wave_last) pv_product(i & (kPfStages - 1));
-            if (next_vis) softmax_tile(tile + 1, (i + 1) & (kPfStages - 1));
+            if (next_vis) softmax_tile(tile + 1, (i + 1) & (kPfStages - 1), false);
         };
 
         if (ntiles > 0) {
@@ -1041,7 +1057,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                         qop[nb][dc][w] = T::pack(T::lo(qop[nb][dc][w]) * a.scale_log2, T::hi(qop[nb][dc][w]) * a.scale_log2);
             if (key0 <= wave_last) {
                 s_product(0);
-                softmax_tile(t_begin, 0);
+                softmax_tile(t_begin, 0, true);
                 pv_product(0);
             }
             // Pairs of steps (i0, i0+1), i0 even: barrier B publishes K of
