@@ -69,6 +69,7 @@ namespace {
 constexpr int kPfWaves = 8;
 constexpr int kPfThreads = kPfWaves * kWave;
 constexpr int kPfStages = 4;              // LDS ring of K/V tiles
+constexpr int kArriveSpinLimit = 1 << 18; // polls (each with a 64-cycle sleep) of a split-barrier wait
 constexpr int kTileBytes = 16384;         // one K (or V) tile in LDS, every tile shape
 constexpr int kPfMaxKeys = 64;            // keys per tile, largest tile shape
 
@@ -400,8 +401,11 @@ constexpr int kPagesPerTile = 2;
 struct PrefillLds {
     alignas(16) uint8_t k[kPfStages][kTileBytes];
     alignas(16) uint8_t v[kPfStages][kTileBytes];
-    alignas(16) float b[kPfStages][kPfMaxKeys];
+    // Key biases (0 or -inf) of partial tiles: the pipelined loop indexes
+    // them by tile mod 8, the other loop by its ring stage.
+    alignas(16) float b[2 * kPfStages][kPfMaxKeys];
     alignas(16) int full[kPfStages][kPfWaves];
+    int arrive;  // pipelined loop: arrivals of the item's waves (see wait_arrivals)
     uint64_t pick[kPfWaves];  // chunk choice: each wave's best (cost, candidate)
     // The walk's index (num_seqs <= 64): sequence s's metadata, item count
     // and inclusive prefix of item counts.
@@ -841,7 +845,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 const uint8_t* g = reinterpret_cast<const uint8_t*>(kZeroChunk);
                 if (ok) g = cache + base + (int64_t)(key & (a.block_size - 1)) * row_bytes_g + 16 * cidx;
                 lds_dma16(g, lds0 + 1024 * j);
-                if (is_k && lslot == 0) sm_b[st][row] = ok ? 0.f : kNegInf;
+                if (is_k && lslot == 0) sm_b[(tile - t_begin) & (2 * kPfStages - 1)][row] = ok ? 0.f : kNegInf;
             }
         };
         auto issue_k = [&](int tile, int st, int64_t off) {
@@ -941,7 +945,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             const int tile0 = tile * SH::kKeys;
             const bool full = ((full_stages >> st) & 1u) != 0;
             const bool fast = full && tile0 + SH::kKeys - 1 <= wave_first;
-            const float* smb = &sm_b[st][0];
+            const float* smb = &sm_b[(tile - t_begin) & (2 * kPfStages - 1)][0];
             if (!fast) {
 #pragma unroll
                 for (int h = 0; h < SH::kHalves; ++h)
@@ -1011,14 +1015,41 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             }
         };
 
+        // Split barrier of the loop.  A wave arrives (one LDS count) once its
+        // copies issued at the top of the pair have landed and its LDS
+        // reads of the pair's last products have returned; at the top of
+        // the next pair it waits for all arrivals.  Between the two it runs
+        // its last softmax, so waves may drift apart by that much without
+        // waiting (a work-group barrier per pair keeps them in lockstep,
+        // and the two waves of a SIMD then contend for the matrix core and
+        // the vector ALU at the same moments).  The wait is bounded: past
+        // the bound the wave goes on (never reached while every wave runs
+        // the loop, which always arrives).
+        auto arrive_pair = [&]() {
+            wait_vmcnt_all();  // this wave's copies and LDS reads complete
+            asm volatile("" : : : "memory");
+            if (lane == 0) __hip_atomic_fetch_add(&lds.arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        };
+        auto wait_arrivals = [&](int target) {
+            for (int spin = 0; spin < kArriveSpinLimit; ++spin) {
+                const int n = __builtin_amdgcn_readfirstlane(
+                    __hip_atomic_load(&lds.arrive, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (n >= target) break;
+                __builtin_amdgcn_s_sleep(1);
+            }
+            asm volatile("" : : : "memory");  // no LDS access or copy moves above the wait
+        };
+
         // Step i: S^T of tile i+1, O^T += V^T P^T of tile i (step 0: done
         // in the prologue), then the probabilities of tile i+1 (products
-        // skipped for tiles past the wave's last visible key).
-        auto step = [&](int i, bool pv) __attribute__((always_inline)) {
+        // skipped for tiles past the wave's last visible key).  `last`: the
+        // pair's second step, which arrives after its products.
+        auto step = [&](int i, bool pv, bool last) __attribute__((always_inline)) {
             const int tile = t_begin + i;
             const bool next_vis = i + 1 < ntiles && (tile + 1) * SH::kKeys <= wave_last;
             if (next_vis) s_product((i + 1) & (kPfStages - 1));
             if (pv && tile * SH::kKeys <= wave_last) pv_product(i & (kPfStages - 1));
+            if (last) arrive_pair();
             if (next_vis) softmax_tile(tile + 1, (i + 1) & (kPfStages - 1), false);
         };
 
@@ -1035,6 +1066,7 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             issue_k(t_begin, 0, off0);
             issue_v(t_begin, 0, off0);
             if (t_begin + kWave < t_end) next_pages = window_pages(t_begin + kWave);
+            if (threadIdx.x == 0) lds.arrive = 0;  // no wave counts before the next barrier
             landed_barrier();
             tile_offs = window_offsets(tile_pages, tile_base);
             int64_t pend = -1;  // offset of the last K tile issued, whose V is still to come
@@ -1060,11 +1092,18 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                 softmax_tile(t_begin, 0, true);
                 pv_product(0);
             }
-            // Pairs of steps (i0, i0+1), i0 even: barrier B publishes K of
-            // i0+1, i0+2 and V of i0, i0+1; then the copies of K i0+3, i0+4
-            // and V i0+2, i0+3 go out (their stages were last read before B).
+            // Pairs of steps (i0, i0+1), i0 even: the sync at the top (the
+            // work-group barrier for the first pair, then the arrivals of
+            // the previous pair) publishes K of i0+1, i0+2 and V of i0, i0+1;
+            // then the copies of K i0+3, i0+4 and V i0+2, i0+3 go out: their
+            // stages were last read by the products of the previous pair,
+            // before every wave arrived.  Partial-tile biases are written at
+            // issue time into slot tile mod 8: K i0+4's bias then replaces
+            // tile i0-4's, not tile i0's (read by softmax i0, which a wave
+            // runs after its arrival).
             for (int i0 = 0; i0 < ntiles; i0 += 2) {
-                landed_barrier();
+                if (i0 == 0) landed_barrier();
+                else wait_arrivals(kPfWaves * (i0 / 2));
                 if (i0 + 2 < ntiles) {
                     int64_t off3 = -1, off4 = -1;
                     if (i0 + 3 < ntiles) {
@@ -1081,8 +1120,8 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
                     if (i0 + 3 < ntiles) issue_v(t_begin + i0 + 3, (i0 + 3) & (kPfStages - 1), off3);
                     pend = off4;
                 }
-                step(i0, i0 > 0);
-                if (i0 + 1 < ntiles) step(i0 + 1, true);
+                step(i0, i0 > 0, false);
+                if (i0 + 1 < ntiles) step(i0 + 1, true, true);
             }
         }
     } else {
