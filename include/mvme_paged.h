@@ -118,7 +118,11 @@ int mvme_gather_kv_cache(void* key_out, void* value_out,
 /*
  * Bytes of device workspace mvme_paged_attention needs for these shapes
  * (0 when no split-K merge is required).  Pure host function.
- * partition_tokens: 0 selects the library's default partition size.
+ * partition_tokens: 0 selects the library's plan; > 0 forces split-K
+ * partitions of that many tokens; -1 forces the balanced walk (batch <= 256:
+ * every (sequence, kv head) unit laid end to end and cut into equal shares of
+ * tokens, one per work-group, the units cut by a share boundary merged from
+ * their pieces).
  */
 size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                            int64_t head_dim, int64_t block_size,
@@ -132,7 +136,7 @@ size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_heads, int64
  * Sequences with context_lens[b] <= 0 or beyond the table capacity produce
  * zeros; out-of-range pages are skipped.  fp32 accumulation, fp32 split-K
  * merge.  `workspace` must hold mvme_paged_attention_workspace_size(...)
- * bytes (may be NULL when that is 0).
+ * bytes (may be NULL when that is 0); partition_tokens as there.
  * Replaces: paged_attention_cuda, attention_vector128, attention_partition
  *   and merge_partitions (mini_engine/kernels/csrc/paged_attention.cu:52-280),
  *   bound as extension.paged_attention (csrc/bindings.cpp:152-184, :196-199)

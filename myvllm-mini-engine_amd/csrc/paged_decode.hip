@@ -89,13 +89,76 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
     if (owns_dim) static_cast<uint16_t*>(a.out)[bh * D + tid] = T::from_float(sum > 0.f ? o / sum : 0.f);
 }
 
+// Merge of the balanced walk: work-group l merges the unit whose last chunk
+// lies in share l when that unit began in an earlier share.  The unit's
+// pieces are the shares from the one holding its first chunk up to l; the
+// first of them wrote its piece as its share's last segment (row slot 1)
+// unless the share began with the unit, every later one as its share's first
+// segment (slot 0).  Shares left empty (fewer chunks than work-groups) wrote
+// nothing and are skipped.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(kLptMax) void paged_decode_flat_merge_kernel(DecodeArgs a) {
+    __shared__ int fl_len[kLptMax];
+    __shared__ int fl_pref[kLptMax + 1];
+    __shared__ int fl_tot[kLptMax / kWave];
+    flat_prefix(a, DecodeShape<D>::kTpi, fl_len, fl_pref, fl_tot);
+    const int ng = a.flat_groups;
+    const int64_t l = blockIdx.x;
+    const int per_seq = a.kv_heads * a.gtiles;
+    const int64_t wc = fl_pref[a.batch];
+    const int64_t total = wc * per_seq;
+    const int64_t s0 = flat_share_start(l, total, ng);
+    const int64_t s1 = flat_share_start(l + 1, total, ng);
+    if (s0 >= s1) return;
+    const int r = (int)(s0 / wc);
+    const int b = flat_seq_of(fl_pref, a.batch, s0 - r * wc);
+    const int64_t first = r * wc + fl_pref[b];
+    const int64_t last = r * wc + fl_pref[b + 1];
+    if (first == s0 || last > s1) return;  // not cut, or its last piece is later
+    const int64_t p0 = ((first + 1) * ng - 1) / total;  // share holding chunk `first`
+    const int kvh = r / a.gtiles;
+    const int h0 = kvh * a.group + (r - kvh * a.gtiles) * G;
+    auto row_of = [&](int64_t p, int g) __attribute__((always_inline)) -> int64_t {
+        const int slot = p == p0 && flat_share_start(p, total, ng) < first ? 1 : 0;
+        return (p * 2 + slot) * G + g;
+    };
+    auto empty = [&](int64_t p) __attribute__((always_inline)) {
+        return flat_share_start(p, total, ng) == flat_share_start(p + 1, total, ng);
+    };
+    for (int idx = threadIdx.x; idx < G * D; idx += kLptMax) {
+        const int g = idx / D;
+        const int d = idx - g * D;
+        float mx = kNegInf;
+        for (int64_t p = p0; p <= l; ++p)
+            if (!empty(p)) mx = fmaxf(mx, a.ws_ml[row_of(p, g) * 2]);
+        const float ref = mx == kNegInf ? 0.f : mx;
+        float sum = 0.f, o = 0.f;
+        for (int64_t p = p0; p <= l; ++p) {
+            if (empty(p)) continue;
+            const int64_t row = row_of(p, g);
+            const float w = fast_exp2(a.ws_ml[row * 2] - ref);
+            sum += a.ws_ml[row * 2 + 1] * w;
+            o += a.ws_acc[row * D + d] * w;
+        }
+        static_cast<uint16_t*>(a.out)[((int64_t)b * a.q_heads + h0 + g) * D + d] =
+            T::from_float(sum > 0.f ? o / sum : 0.f);
+    }
+}
+
 struct DecodePlan {
     int partition;
     int max_parts;
     int gtile;  // G of the kernel instance
     int waves;  // waves per work-group (kSplitWaves, kWholeWaves or kLongWaves)
     bool stream;  // non-temporal K/V loads
+    int flat_groups;  // > 0: balanced walk with this many work-groups
 };
+
+// Balanced walk: work-groups (a multiple of 8, the XCD count) and their
+// waves.  Measured on 32 sequences of contexts U[1,4096] (fp16, block 256, µs
+// per call): 256 x 8 waves 62.5, 256 x 16 63.3, 512 x 8 63.3, 1024 x 4 67.9.
+constexpr int kFlatGroups = 256;
+constexpr int kFlatWaves = kWholeWaves;
 
 constexpr int64_t kStreamBytes = int64_t(64) << 20;  // K+V bytes within capacity above which loads stream
 
@@ -164,6 +227,23 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     }
     p.partition = (int)part;
     p.max_parts = (int)((cap + part - 1) / part);
+    // One round of long units (at most one per CU, each of the 16-wave
+    // regime), or a request (requested == -1), takes the balanced walk:
+    // there, one work-group per unit leaves the CUs holding the shortest
+    // units idle while the longest stream alone, whatever the order.  32
+    // sequences of contexts U[1,4096] (fp16, block 256): 70.5 -> 62.5 µs per
+    // call; all 4096 tokens: 84.3 -> 84.6.  With two or more units per CU the
+    // longest-first order already balances the CUs, and the walk was slower
+    // (64 sequences U[1,4096] sharing a 1024-token prefix, bf16, block 16:
+    // 88.1 -> 90.5 µs; 128 sequences U[1,4096]: 166.4 -> 169.2).
+    const bool flat = batch <= kLptMax &&
+                      (requested == -1 ||
+                       (requested <= 0 && whole && p.waves == kLongWaves && units <= kDeviceCUs));
+    if (flat) {
+        p.flat_groups = kFlatGroups;
+        p.waves = kFlatWaves;
+        p.max_parts = 1;
+    }
     // In floating point: the size query runs before any shape check, where the
     // integer product could overflow.
     p.stream = (double)batch * (double)cap * (double)kv_heads * (double)head_dim * 4.0 > (double)kStreamBytes;
@@ -183,7 +263,7 @@ void launch_decode_kernel_pro(const DecodeArgs& a, dim3 grid, bool page_uniform,
 
 template <typename T, int D, int G, int NW>
 void launch_decode_nw(const DecodeArgs& a, int units, bool page_uniform, bool stream, hipStream_t s) {
-    const dim3 grid(units, a.max_parts);
+    const dim3 grid(a.flat_groups > 0 ? a.flat_groups : units, a.max_parts);
     if (stream) {
         launch_decode_kernel_pro<T, D, G, NW, true>(a, grid, page_uniform, s);
         return;
@@ -196,7 +276,9 @@ void launch_decode(const DecodeArgs& a, const DecodePlan& p, int units, bool pag
     if (p.waves == kLongWaves) launch_decode_nw<T, D, G, kLongWaves>(a, units, page_uniform, p.stream, s);
     else if (p.waves == kWholeWaves) launch_decode_nw<T, D, G, kWholeWaves>(a, units, page_uniform, p.stream, s);
     else launch_decode_nw<T, D, G, kSplitWaves>(a, units, page_uniform, p.stream, s);
-    if (a.max_parts > 1)
+    if (a.flat_groups > 0)
+        hipLaunchKernelGGL((paged_decode_flat_merge_kernel<T, D, G>), dim3(a.flat_groups), dim3(kLptMax), 0, s, a);
+    else if (a.max_parts > 1)
         hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(units / a.kv_heads / a.gtiles * a.q_heads),
                            dim3(merge_threads<D>()), 0, s, a);
 }
@@ -261,6 +343,7 @@ extern "C" size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_h
         return 0;
     const DecodePlan p = make_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, table_width,
                                           partition_tokens);
+    if (p.flat_groups > 0) return (size_t)p.flat_groups * 2 * p.gtile * (head_dim + 2) * sizeof(float);
     if (p.max_parts <= 1) return 0;
     return (size_t)batch * q_heads * p.max_parts * (head_dim + 2) * sizeof(float);
 }
@@ -302,7 +385,8 @@ int launch_paged_attention(void* out, const void* query, const void* key_cache, 
     a.lens = context_lens;
     if (need > 0) {
         a.ws_acc = static_cast<float*>(workspace);
-        a.ws_ml = a.ws_acc + batch * q_heads * p.max_parts * head_dim;
+        a.ws_ml = a.ws_acc + (p.flat_groups > 0 ? (int64_t)p.flat_groups * 2 * p.gtile
+                                                 : batch * q_heads * p.max_parts) * head_dim;
     }
     a.q_heads = (int)q_heads;
     a.kv_heads = (int)kv_heads;
@@ -315,7 +399,9 @@ int launch_paged_attention(void* out, const void* query, const void* key_cache, 
     a.capacity = (int)(table_width * block_size);
     a.partition = p.partition;
     a.max_parts = p.max_parts;
-    a.lpt_batch = p.max_parts == 1 && batch >= 2 && batch <= kLptMax ? (int)batch : 0;
+    a.lpt_batch = p.flat_groups == 0 && p.max_parts == 1 && batch >= 2 && batch <= kLptMax ? (int)batch : 0;
+    a.flat_groups = p.flat_groups;
+    a.batch = (int)batch;
     a.scale_log2 = kLog2e / sqrtf((float)head_dim);
     if (pro && pro->mode != 0) {
         a.prologue = pro->mode;

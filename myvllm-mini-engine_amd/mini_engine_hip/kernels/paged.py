@@ -74,7 +74,8 @@ def paged_attention(query, key_cache, value_cache, block_tables, context_lens, b
     block_tables [B, W] int64 (-1 padding past the active pages);
     context_lens [B] int64.  Returns [B, Hq, D] in the query dtype.
 
-    ``partition_tokens`` (0 = library default) sets the split-K partition;
+    ``partition_tokens`` (0 = library plan) sets the split-K partition, or
+    with -1 forces the balanced walk (equal shares of tokens per work-group);
     ``out`` / ``workspace`` let a caller supply preallocated buffers.
     """
     if backend != "hip":

@@ -104,6 +104,57 @@ def test_split_merge_over_several_weight_windows():
     assert max_err(split, oracle(args)) <= GATE[torch.float16]
 
 
+def ragged_lengths(batch, high, seed):
+    gen = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(1, high + 1, (batch,), generator=gen)
+    lengths[0] = high  # one unit spans several shares
+    lengths[-1] = 1
+    return tuple(lengths.tolist())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dim,heads,kv_heads,lengths,block_size", [
+    (128, 16, 8, ragged_lengths(32, 4096, 1), 16),    # the plan's own pick (256 long units)
+    (128, 16, 8, (1, 5), 16),                        # fewer chunks than work-groups: empty shares
+    (64, 16, 4, ragged_lengths(256, 600, 2), 16),    # 256 sequences, 4-head tiles
+    (256, 8, 8, (3000, 17, 1, 4096, 900), 32),       # group 1, head dim 256
+    (80, 12, 4, (100, 2000, 3), 7),                  # group 3, pages not a multiple of the wave tile
+    (16, 32, 8, ragged_lengths(9, 5000, 3), 64),     # head dim 16: 128-token chunks
+])
+def test_balanced_walk_matches_oracle(dtype, dim, heads, kv_heads, lengths, block_size):
+    """Balanced walk: units laid end to end and cut into equal shares per
+    work-group; units cut by a share boundary are merged from their pieces.
+    Forced with partition_tokens=-1; the 32-sequence case also takes it by
+    the library's plan."""
+    args = decode_inputs(dtype, head_dim=dim, heads=heads, kv_heads=kv_heads, lengths=lengths,
+                         block_size=block_size, seed=len(lengths) + dim)
+    dev = to_dev(args)
+    print(f"balanced walk {dtype} D={dim} {heads}/{kv_heads} B={len(lengths)} block={block_size}", flush=True)
+    walk = paged_attention(*dev, backend="hip", partition_tokens=-1)
+    expected = oracle(args)
+    assert max_err(walk, expected) <= GATE[dtype]
+    single = paged_attention(*dev, backend="hip", partition_tokens=1 << 20)
+    assert (walk.float() - single.float()).abs().max().item() <= GATE[dtype]
+    if len(lengths) == 32:
+        assert torch.equal(paged_attention(*dev, backend="hip"), walk)
+
+
+def test_balanced_walk_trusted_empty_and_invalid_rows():
+    """Trusted mode on the walk: contexts of 0 or beyond the capacity and
+    all-absent pages give zeros; the other sequences are unaffected."""
+    lengths = (700, 1, 2048, 300)
+    args = decode_inputs(torch.bfloat16, lengths=lengths, block_size=16, seed=77)
+    dev = to_dev(args)
+    dev[4][1] = 0
+    dev[4][3] = 10**6
+    dev[3][2].fill_(-1)
+    actual = paged_attention(*dev, backend="hip", validate=False, partition_tokens=-1)
+    assert torch.isfinite(actual).all()
+    assert not actual[1:4].any()
+    alone = paged_attention(dev[0][:1], dev[1], dev[2], dev[3][:1], dev[4][:1], 16, backend="hip")
+    assert (actual[0].float() - alone[0].float()).abs().max().item() <= GATE[torch.bfloat16]
+
+
 @pytest.mark.parametrize("batch,block_size,low,high", [(2, 256, 40000, 40001), (40, 16, 1500, 2600)])
 def test_streaming_loads_match_oracle(batch, block_size, low, high):
     """Calls with more than 64 MiB of K/V within the tables' capacity load

@@ -128,6 +128,20 @@ def test_split_k_and_head_dims(rope, head_dim):
     check_equal(step, 16, rope, partition_tokens=0)
 
 
+@pytest.mark.parametrize("rope", [False, True])
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_balanced_walk(rope, head_dim):
+    """The balanced walk (units cut into equal shares per work-group): the
+    share holding position len - 1 writes the row, the share that starts the
+    unit writes the rotated query."""
+    gen = torch.Generator().manual_seed(head_dim)
+    lengths = torch.randint(1, 3001, (24,), generator=gen)
+    lengths[0] = 3000
+    step = make_step(24, 16, 8, head_dim, 16, lengths.tolist(), torch.bfloat16, seed=head_dim + 1)
+    print(f"decode write balanced walk rope={rope} D={head_dim}", flush=True)
+    check_equal(step, 16, rope, partition_tokens=-1)
+
+
 @pytest.mark.parametrize("q_heads,kv_heads", [(8, 8), (32, 8), (64, 8), (28, 4)])
 def test_gqa_tiles(q_heads, kv_heads):
     """Group 1, 4, 8 (two 4-head tiles, both writing the same rows) and 7."""
