@@ -1090,20 +1090,23 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
             if (key0 <= wave_last) {
                 s_product(0);
                 softmax_tile(t_begin, 0, true);
-                pv_product(0);
             }
-            // Pairs of steps (i0, i0+1), i0 even: the sync at the top (the
-            // work-group barrier for the first pair, then the arrivals of
-            // the previous pair) publishes K of i0+1, i0+2 and V of i0, i0+1;
-            // then the copies of K i0+3, i0+4 and V i0+2, i0+3 go out: their
-            // stages were last read by the products of the previous pair,
-            // before every wave arrived.  Partial-tile biases are written at
+            // The prologue's arrival: this wave's copies of K 1, 2 and V 1
+            // have landed and its reads of K 0 are done.  Tile 0's O^T
+            // product follows, so the first pair waits for no wave's O^T
+            // (V 0's stage is next refilled two pairs on).
+            arrive_pair();
+            if (key0 <= wave_last) pv_product(0);
+            // Pairs of steps (i0, i0+1), i0 even: the arrivals at the top
+            // (the prologue's for the first pair, then the previous pair's)
+            // publish K of i0+1, i0+2 and V of i0, i0+1; then the copies of
+            // K i0+3, i0+4 and V i0+2, i0+3 go out: their stages were last
+            // read by products that every wave finished before arriving.  Partial-tile biases are written at
             // issue time into slot tile mod 8: K i0+4's bias then replaces
             // tile i0-4's, not tile i0's (read by softmax i0, which a wave
             // runs after its arrival).
             for (int i0 = 0; i0 < ntiles; i0 += 2) {
-                if (i0 == 0) landed_barrier();
-                else wait_arrivals(kPfWaves * (i0 / 2));
+                wait_arrivals(kPfWaves * (i0 / 2 + 1));
                 if (i0 + 2 < ntiles) {
                     int64_t off3 = -1, off4 = -1;
                     if (i0 + 3 < ntiles) {
