@@ -154,11 +154,11 @@ struct DecodePlan {
     int flat_groups;  // > 0: balanced walk with this many work-groups
 };
 
-// Balanced walk: work-groups (a multiple of 8, the XCD count) and their
-// waves.  Measured on 32 sequences of contexts U[1,4096] (fp16, block 256, µs
-// per call): 256 x 8 waves 62.5, 256 x 16 63.3, 512 x 8 63.3, 1024 x 4 67.9.
+// Balanced walk: work-groups (a multiple of 8, the XCD count; kFlatWaves
+// waves each).  Measured on 32 sequences of contexts U[1,4096] (fp16, block
+// 256, µs per call): 256 x 8 waves 62.5, 256 x 16 63.3, 512 x 8 63.3,
+// 1024 x 4 67.9.
 constexpr int kFlatGroups = 256;
-constexpr int kFlatWaves = kWholeWaves;
 
 constexpr int64_t kStreamBytes = int64_t(64) << 20;  // K+V bytes within capacity above which loads stream
 
@@ -182,7 +182,8 @@ constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 // capacity only).  Enough (sequence, kv head) units to occupy every CU, a
 // capacity of one 16-wave step, or two steps with more than a quarter of the
 // CUs' worth of units: one work-group per unit over the whole context, merged
-// in LDS (8 waves, 16 for units of at least kLongUnitBytes).  Otherwise split-K into partitions of 4-wave work-groups, sized to
+// in LDS (8 waves, 16 for units of at least kLongUnitBytes; below two
+// 16-wave steps 8, or 4 with more units than CUs).  Otherwise split-K into partitions of 4-wave work-groups, sized to
 // give every CU about two work-groups (at least one 4-wave step each), plus
 // a merge kernel.  `requested` > 0 forces split-K with that partition length
 // (rounded to the wave tiling).
@@ -211,7 +212,14 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     const bool whole = units >= kDeviceCUs - kDeviceCUs / 16 || cap <= whole_step ||
                        (cap <= 2 * whole_step && units > kDeviceCUs / 4);
     if (requested <= 0 && whole) {
-        p.waves = cap < 2 * whole_step ? kSplitWaves : cap * head_dim * 4 >= kLongUnitBytes ? kLongWaves : kWholeWaves;
+        // Below two 16-wave steps: 8 waves (a 128-token context in one
+        // iteration of loads) while the units fit the CUs, 4 beyond (more
+        // work-groups per CU).  µs per call: B1 / ctx 128 fp16 4.85 -> 4.77,
+        // B4 / ctx 256 6.82 -> 6.00, B32 / ctx 256 bf16 8.76 -> 7.32; but
+        // B64 / ctx 128 7.18 -> 7.39 (512 units), hence 4 there.
+        const int short_waves = units <= kDeviceCUs ? kWholeWaves : kSplitWaves;
+        p.waves = cap < 2 * whole_step ? short_waves
+                  : cap * head_dim * 4 >= kLongUnitBytes ? kLongWaves : kWholeWaves;
         part = (cap + tile - 1) / tile * tile;
     } else {
         p.waves = kSplitWaves;
@@ -245,8 +253,9 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
         p.max_parts = 1;
     }
     // In floating point: the size query runs before any shape check, where the
-    // integer product could overflow.
-    p.stream = (double)batch * (double)cap * (double)kv_heads * (double)head_dim * 4.0 > (double)kStreamBytes;
+    // integer product could overflow.  The walk's kernels always load with the
+    // non-temporal hint.
+    p.stream = flat || (double)batch * (double)cap * (double)kv_heads * (double)head_dim * 4.0 > (double)kStreamBytes;
     return p;
 }
 

@@ -55,6 +55,9 @@ constexpr int64_t kLongUnitBytes = int64_t(2) << 20;
 constexpr int kLptMax = 256;     // largest batch whose units go longest context first
 static_assert(kSplitWaves * kWave >= kLptMax, "one thread per sequence key");
 constexpr int kDecodeLoads = 4;  // K (and V) loads per lane per iteration
+// Balanced walk: waves per work-group (its own kernel instances, with
+// non-temporal loads: the plan takes the walk for calls of 480 MiB or more).
+constexpr int kFlatWaves = kWholeWaves;
 
 template <int D>
 struct DecodeShape {
@@ -179,8 +182,9 @@ __device__ inline int flat_seq_of(const int* pref, int n, int64_t cin) {
 __device__ inline int64_t flat_share_start(int64_t l, int64_t total, int groups) { return l * total / groups; }
 
 // PRO: the kernel runs the fused prologue (a.prologue 1 or 2); without it
-// the prologue's code is not compiled in.
-template <typename T, int D, int G, bool PAGE_UNIFORM, int NW, bool STREAM, bool PRO>
+// the prologue's code is not compiled in.  FLAT: the balanced walk (its
+// segment loop would cost the other modes about 20 VGPRs).
+template <typename T, int D, int G, bool PAGE_UNIFORM, int NW, bool STREAM, bool PRO, bool FLAT>
 __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) {
     using S = DecodeShape<D>;
     constexpr int L = kDecodeLoads;
@@ -204,14 +208,17 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     __shared__ int fl_pref[kLptMax + 1];
     __shared__ int fl_tot[kLptMax / kWave];
     int64_t fl_wc = 0, fl_pos = 0, fl_stop = 0, fl_row = 0, fl_row_later = 0;
-    if (a.flat_groups > 0) {
+    if constexpr (FLAT) {
         flat_prefix(a, S::kTpi, fl_len, fl_pref, fl_tot);
         const int ng = a.flat_groups;
         // Work-groups go to the 8 XCDs round robin; consecutive shares run
         // on one XCD, so a column's rows (and the pages its sequences
         // share) meet in one L2.
         const int l = (unit & 7) * (ng >> 3) + (unit >> 3);
-        fl_wc = fl_pref[a.batch];
+        // LDS reads are wave-uniform here; readfirstlane keeps the segment
+        // bounds in scalar registers (uniform loop control, as for the other
+        // modes).
+        fl_wc = __builtin_amdgcn_readfirstlane(fl_pref[a.batch]);
         const int64_t total = fl_wc * per_seq;
         fl_pos = flat_share_start(l, total, ng);
         fl_stop = flat_share_start(l + 1, total, ng);
@@ -284,11 +291,11 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     }
 
     for (;;) {
-        if (a.flat_groups > 0) {
+        if constexpr (FLAT) {
             // Chunks [first, last) of the column are this unit's.
-            const int64_t first = (int64_t)r * fl_wc + fl_pref[b];
-            const int64_t last = (int64_t)r * fl_wc + fl_pref[b + 1];
-            len = fl_len[b];
+            const int64_t first = (int64_t)r * fl_wc + __builtin_amdgcn_readfirstlane(fl_pref[b]);
+            const int64_t last = (int64_t)r * fl_wc + __builtin_amdgcn_readfirstlane(fl_pref[b + 1]);
+            len = __builtin_amdgcn_readfirstlane(fl_len[b]);
             start = (int)(fl_pos - first) * S::kTpi;
             end = min((int)(min(fl_stop, last) - first) * S::kTpi, len);
             direct = fl_pos == first && last <= fl_stop;
@@ -551,7 +558,7 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
             if (direct) {
                 static_cast<uint16_t*>(a.out)[bh * D + d] = T::from_float(sum > 0.f ? o / sum : 0.f);
             } else {
-                const int64_t row = a.flat_groups > 0 ? fl_row + g : bh * a.max_parts + part;
+                const int64_t row = FLAT ? fl_row + g : bh * a.max_parts + part;
                 a.ws_acc[row * D + d] = o;
                 if (d == 0) {
                     a.ws_ml[row * 2] = mx;
@@ -559,10 +566,10 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
                 }
             }
         }
-        if (a.flat_groups == 0) return;
+        if constexpr (!FLAT) return;
         // The share's next unit: the column's next sequence, or the first
         // sequence of the next column.
-        fl_pos = (int64_t)r * fl_wc + fl_pref[b + 1];
+        fl_pos = (int64_t)r * fl_wc + __builtin_amdgcn_readfirstlane(fl_pref[b + 1]);
         if (fl_pos >= fl_stop) return;
         fl_row = fl_row_later;
         if (++b == a.batch) {
@@ -575,10 +582,23 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
 
 template <typename T, int D, int G, int NW, bool STREAM, bool PRO>
 void launch_decode_kernel(const DecodeArgs& a, dim3 grid, bool page_uniform, hipStream_t s) {
+    if constexpr (NW == kFlatWaves && STREAM) {
+        if (a.flat_groups > 0) {
+            if (page_uniform)
+                hipLaunchKernelGGL((paged_decode_kernel<T, D, G, true, NW, true, PRO, true>), grid, dim3(NW * kWave),
+                                   0, s, a);
+            else
+                hipLaunchKernelGGL((paged_decode_kernel<T, D, G, false, NW, true, PRO, true>), grid, dim3(NW * kWave),
+                                   0, s, a);
+            return;
+        }
+    }
     if (page_uniform)
-        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, true, NW, STREAM, PRO>), grid, dim3(NW * kWave), 0, s, a);
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, true, NW, STREAM, PRO, false>), grid, dim3(NW * kWave), 0, s,
+                           a);
     else
-        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, false, NW, STREAM, PRO>), grid, dim3(NW * kWave), 0, s, a);
+        hipLaunchKernelGGL((paged_decode_kernel<T, D, G, false, NW, STREAM, PRO, false>), grid, dim3(NW * kWave), 0,
+                           s, a);
 }
 
 // Head dims with a fused-prologue instantiation (one 16-byte chunk per lane).
