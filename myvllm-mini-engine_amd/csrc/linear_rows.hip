@@ -17,9 +17,10 @@
 // accumulation), then the 16 partial tiles are summed through LDS and
 // rounded once to the output type.  Measured over 28 layers' distinct
 // 2048 x 2048 bf16 weights at 32 rows: register kernel 7.8 us per call,
-// staged kernel 5.9 us (x re-read from L2 by every work-group dominated the
+// staged kernel 5.5 us (x re-read from L2 by every work-group dominated the
 // register kernel: 5.6 us with the weight loads removed, 4.3 us with the
-// x loads removed).
+// x loads removed; with 8 features per work-group, as the staged kernel
+// has, it took 7.7 us).
 #include <mutex>
 
 #include "mvme_common.h"
@@ -164,18 +165,21 @@ __global__ __launch_bounds__(kLinThreads) void linear_rows_staged_kernel(LinearA
     const int row_instr = row_chunks / 64;  // 1 KiB copies per row
     uint8_t* xs = smem;
     uint8_t* ws = smem + (size_t)16 * MB * K * 2;
+    // The weight slab first: its copies come from HBM, x's from L2 (every
+    // work-group reads the same x), so the longer latency starts first
+    // (5.9 -> 5.5 us per call at 32 x 2048 x 2048).
+    for (int i = wave; i < kStagedFeat * row_instr; i += kLinWaves) {
+        const int r = i / row_instr, cbase = (i % row_instr) * 64;
+        const int c = (cbase + lane) ^ (r & 7);
+        const uint16_t* src = static_cast<const uint16_t*>(a.weight) + (int64_t)(n0 + r) * K + 8 * c;
+        lds_copy16(src, lds_offset(ws) + (uint32_t)(r * row_chunks + cbase) * 16);
+    }
     // Rows of x past M copy row 0 (in bounds); their products are dropped.
     for (int i = wave; i < 16 * MB * row_instr; i += kLinWaves) {
         const int r = i / row_instr, cbase = (i % row_instr) * 64;
         const int c = (cbase + lane) ^ (r & 15);
         const uint16_t* src = static_cast<const uint16_t*>(a.x) + (int64_t)(r < a.rows ? r : 0) * a.x_stride + 8 * c;
         lds_copy16(src, lds_offset(xs) + (uint32_t)(r * row_chunks + cbase) * 16);
-    }
-    for (int i = wave; i < kStagedFeat * row_instr; i += kLinWaves) {
-        const int r = i / row_instr, cbase = (i % row_instr) * 64;
-        const int c = (cbase + lane) ^ (r & 7);
-        const uint16_t* src = static_cast<const uint16_t*>(a.weight) + (int64_t)(n0 + r) * K + 8 * c;
-        lds_copy16(src, lds_offset(ws) + (uint32_t)(r * row_chunks + cbase) * 16);
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's copies landed
     __syncthreads();                // everyone's
