@@ -182,11 +182,12 @@ constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 // capacity only).  Enough (sequence, kv head) units to occupy every CU, a
 // capacity of one 16-wave step, or two steps with more than a quarter of the
 // CUs' worth of units: one work-group per unit over the whole context, merged
-// in LDS (8 waves, 16 for units of at least kLongUnitBytes; below two
-// 16-wave steps 8, or 4 with more units than CUs).  Otherwise split-K into partitions of 4-wave work-groups, sized to
-// give every CU about two work-groups (at least one 4-wave step each), plus
-// a merge kernel.  `requested` > 0 forces split-K with that partition length
-// (rounded to the wave tiling).
+// in LDS (8 waves, 16 for units of at least kLongUnitBytes; below two 16-wave
+// steps 8, or 4 with more units than CUs), or, for one round of long units,
+// the balanced walk.  Otherwise split-K into partitions of 4-wave
+// work-groups, sized to give every CU about two work-groups (at least one
+// 4-wave step each), plus a merge kernel.  `requested` > 0 forces split-K with
+// that partition length (rounded to the wave tiling), -1 the balanced walk.
 //
 // Measured at head_dim 128 (bf16, block 16, 16/8 heads, µs per call in a
 // graph): whole-sequence against split-K at 64/128/256 keys.
