@@ -497,6 +497,28 @@ def _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra):
         "frac_of_hbm_peak_unique": unique / per_call / 1e9 / HBM_PEAK_GBS,
         "GBps_logical": logical / per_call / 1e9, "unique_rows": c["unique_rows"], "logical_rows": c["logical_rows"],
         "max_abs_error": err}
+    del c, out
+    # Ragged B=32, ctx U[1,4096], fp16, block 256: one unit per CU, each of
+    # the 16-wave regime, so the plan takes the balanced walk.
+    r = workloads.ragged_decode_case(device=dev)
+    rout = torch.empty_like(r["query"])
+    fnr = lambda: paged_attention(r["query"], r["key_cache"], r["value_cache"], r["block_tables"],  # noqa: E731
+                                  r["context_lens"], 256, backend="hip", validate=False, out=rout)
+
+    def manyr(n=10):
+        def run():
+            for _ in range(n):
+                fnr()
+        return run
+    ms, _ = graph_time_ms(manyr(), torch, calls_per_graph=10, replays=10, warmup=2)
+    per_call = ms / 10 * 1e-3
+    rows = int(r["context_lens"].sum())
+    nbytes = rows * 4096 + 2 * 32 * 16 * 128 * 2 + 32 * 16 * 8 + 32 * 8
+    err = None if cpu is None else max_abs(rout, cpu.decode({k: r[k].cpu() for k in DECODE_NAMES}, 256))
+    extra["ragged_b32_ctx4096_fp16_balanced_walk"] = {
+        "us_per_call": per_call * 1e6, "GBps": nbytes / per_call / 1e9,
+        "frac_of_hbm_peak": nbytes / per_call / 1e9 / HBM_PEAK_GBS, "rows": rows, "algorithmic_bytes": nbytes,
+        "max_abs_error": err}
 
 
 def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra):

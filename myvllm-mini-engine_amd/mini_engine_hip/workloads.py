@@ -74,6 +74,27 @@ def decode_b32_layer(device, seed):
                                device=device)
 
 
+def ragged_decode_case(*, seed=BASE_SEED + 5, device, batch=32, max_len=4096, block_size=256,
+                       dtype=torch.float16):
+    """Ragged decode, contexts U[1, max_len] seeded, every sequence on its own
+    random pages (-1 past its last page)."""
+    gen = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, max_len + 1, (batch,), generator=gen)
+    width = math.ceil(max_len / block_size)
+    pool_pages = batch * width + 7
+    order = torch.randperm(pool_pages, generator=gen)
+    tables = torch.full((batch, width), -1, dtype=torch.int64)
+    for b in range(batch):
+        used = math.ceil(int(lens[b]) / block_size)
+        tables[b, :used] = order[b * width:b * width + used]
+    dgen = _device_generator(device, seed)
+    query = _randn((batch, HEADS, HEAD_DIM), dtype, device, dgen)
+    key = _randn((pool_pages, block_size, KV_HEADS, HEAD_DIM), dtype, device, dgen)
+    value = _randn((pool_pages, block_size, KV_HEADS, HEAD_DIM), dtype, device, dgen)
+    return {"query": query, "key_cache": key, "value_cache": value, "block_tables": tables.to(device),
+            "context_lens": lens.to(torch.int64).to(device), "block_size": block_size}
+
+
 def ragged_shared_prefix_case(*, seed=BASE_SEED + 3, device, batch=64, max_len=4096, block_size=16,
                               shared=16, prefix_tokens=1024, pool_pages=16384, dtype=torch.bfloat16):
     """Ragged decode where `shared` sequences map their first `prefix_tokens`

@@ -281,6 +281,19 @@ def test_c4_ragged_shared_prefix_bf16():
     assert all(torch.equal(tables[i, :64], tables[0, :64]) for i in range(16))
 
 
+def test_ragged_b32_balanced_walk_workload_fp16():
+    """The benchmark's ragged B32 workload (contexts U[1,4096], block 256):
+    one long unit per CU, which the plan hands to the balanced walk."""
+    from mini_engine_hip.workloads import ragged_decode_case
+
+    case = ragged_decode_case(device=DEV)
+    args = [case[n] for n in ("query", "key_cache", "value_cache", "block_tables", "context_lens")] + [256]
+    actual = paged_attention(*args, backend="hip", validate=True)
+    expected = oracle([a.cpu() if isinstance(a, torch.Tensor) else a for a in args])
+    assert max_err(actual, expected) <= GATE[torch.float16]
+    assert torch.equal(paged_attention(*args, backend="hip", partition_tokens=-1), actual)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("dim", [16, 32, 80, 96, 128])
 @pytest.mark.parametrize("partition", [64, 0])
