@@ -182,9 +182,10 @@ constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 // capacity only).  Enough (sequence, kv head) units to occupy every CU, a
 // capacity of one 16-wave step, or two steps with more than a quarter of the
 // CUs' worth of units: one work-group per unit over the whole context, merged
-// in LDS (8 waves, 16 for units of at least kLongUnitBytes; below two 16-wave
-// steps 8, or 4 with more units than CUs), or, for one round of long units,
-// the balanced walk.  Otherwise split-K into partitions of 4-wave
+// in LDS (8 waves, 16 for units of at least kLongUnitBytes unless two 8-wave
+// work-groups per CU hold every unit, which then pair long sequences with
+// short ones; below two 16-wave steps 8, or 4 with more units than CUs), or,
+// for one round of long units, the balanced walk.  Otherwise split-K into partitions of 4-wave
 // work-groups, sized to give every CU about two work-groups (at least one
 // 4-wave step each), plus a merge kernel.  `requested` > 0 forces split-K with
 // that partition length (rounded to the wave tiling), -1 the balanced walk.
@@ -219,8 +220,14 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
         // B4 / ctx 256 6.82 -> 6.00, B32 / ctx 256 bf16 8.76 -> 7.32; but
         // B64 / ctx 128 7.18 -> 7.39 (512 units), hence 4 there.
         const int short_waves = units <= kDeviceCUs ? kWholeWaves : kSplitWaves;
+        // Long units keep 16 waves, except when two 8-wave work-groups per
+        // CU hold every unit at once (units in (CUs, 2 CUs]): the launch
+        // then pairs each long sequence with a short one (lpt_pair).  64
+        // sequences of contexts U[1,4096] sharing a 1024-token prefix (bf16,
+        // block 16): 88.0 -> 81.1 µs; U[1,4096] fp16 block 256: 81.7 -> 77.9.
+        const bool two_per_cu = units > kDeviceCUs && units <= 2 * kDeviceCUs;
         p.waves = cap < 2 * whole_step ? short_waves
-                  : cap * head_dim * 4 >= kLongUnitBytes ? kLongWaves : kWholeWaves;
+                  : cap * head_dim * 4 >= kLongUnitBytes && !two_per_cu ? kLongWaves : kWholeWaves;
         part = (cap + tile - 1) / tile * tile;
     } else {
         p.waves = kSplitWaves;
@@ -410,6 +417,11 @@ int launch_paged_attention(void* out, const void* query, const void* key_cache, 
     a.partition = p.partition;
     a.max_parts = p.max_parts;
     a.lpt_batch = p.flat_groups == 0 && p.max_parts == 1 && batch >= 2 && batch <= kLptMax ? (int)batch : 0;
+    // Two 8-wave work-groups per CU hold every unit at once (units in
+    // (CUs, 2 CUs]): pair long sequences with short ones.  Longest first
+    // alone put the k-th and the (k + batch/2)-th longest on one CU: 64
+    // sequences of contexts U[1,2048] (bf16, block 16) 54.8 -> 47.8 µs.
+    a.lpt_pair = a.lpt_batch > 0 && p.waves == kWholeWaves && units > kDeviceCUs && units <= 2 * kDeviceCUs;
     a.flat_groups = p.flat_groups;
     a.batch = (int)batch;
     a.scale_log2 = kLog2e / sqrtf((float)head_dim);

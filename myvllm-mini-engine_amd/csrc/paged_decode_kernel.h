@@ -90,6 +90,10 @@ struct DecodeArgs {
     int partition;  // tokens per partition (multiple of the wave tile)
     int max_parts;
     int lpt_batch;  // batch size when units go longest sequence first (<= kLptMax), else 0
+    // With two work-groups resident per CU for the whole call: the second
+    // half of the unit groups takes the ranks in reverse (shortest first), so
+    // that each CU pairs a long sequence with a short one.
+    int lpt_pair;
     // Balanced walk (flat_groups > 0, batch <= kLptMax): `flat_groups`
     // work-groups, each taking an equal share of the call's token chunks.
     int flat_groups;
@@ -240,6 +244,8 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
             __shared__ int lpt_keys[kLptMax];
             __shared__ int lpt_pick;
             const int n = a.lpt_batch;
+            const int half = (n + 1) / 2;
+            const int rank = a.lpt_pair && b >= half ? n - 1 - (b - half) : b;
             const int tid = threadIdx.x;
             const int key = tid < n ? (seq_tokens(a.lens[tid], a.capacity) << 8) | (kLptMax - 1 - tid) : -1;
             if (tid < ((n + 3) & ~3)) lpt_keys[tid] = key;  // -1 pads the last group of four
@@ -253,7 +259,7 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
                     g2 += kv.z > key ? 1 : 0;
                     g3 += kv.w > key ? 1 : 0;
                 }
-                if (g0 + g1 + g2 + g3 == b) lpt_pick = tid;
+                if (g0 + g1 + g2 + g3 == rank) lpt_pick = tid;
             }
             __syncthreads();
             b = __builtin_amdgcn_readfirstlane(lpt_pick);
@@ -266,6 +272,8 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
             // holds a key unique to sequence s; its rank is the number of larger
             // keys.  Equal lengths keep the identity order without the count.
             const int n = a.lpt_batch;
+            const int half = (n + 1) / 2;
+            const int rank = a.lpt_pair && b >= half ? n - 1 - (b - half) : b;
             const int key = lane < n ? (seq_tokens(a.lens[lane], a.capacity) << 6) | (63 - lane) : -1;
             const int len0 = __builtin_amdgcn_readlane(key, 0) >> 6;
             if (__ballot(lane < n && (key >> 6) != len0) != 0) {
@@ -278,7 +286,7 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
                     g3 += __builtin_amdgcn_readlane(key, t + 3) > key ? 1 : 0;
                 }
                 for (; t < n; ++t) g0 += __builtin_amdgcn_readlane(key, t) > key ? 1 : 0;
-                b = __builtin_ctzll(__ballot(lane < n && g0 + g1 + g2 + g3 == b));
+                b = __builtin_ctzll(__ballot(lane < n && g0 + g1 + g2 + g3 == rank));
             }
             len = __builtin_amdgcn_readlane(key, b) >> 6;
         } else {

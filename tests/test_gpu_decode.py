@@ -82,6 +82,28 @@ def test_longest_first_unit_order_keeps_each_sequence_its_own_output(batch):
     assert max_err(again, oracle(args2)) <= GATE[torch.float16]
 
 
+@pytest.mark.parametrize("batch,heads,kv_heads,high", [(37, 16, 8, 4096), (64, 16, 8, 4096), (200, 4, 2, 3000)])
+def test_two_work_groups_per_cu_pair_long_with_short(batch, heads, kv_heads, high):
+    """Units in (CUs, 2 CUs]: two 8-wave work-groups per CU hold every unit,
+    and the second half of the unit groups takes the lengths shortest first
+    (odd batch, batch 64, and the LDS ranking of more than 64 sequences):
+    every sequence still gets its own result."""
+    gen = torch.Generator().manual_seed(batch)
+    lengths = torch.randint(1, high + 1, (batch,), generator=gen)
+    lengths[0] = high
+    lengths[1] = 1
+    args = decode_inputs(torch.bfloat16, lengths=tuple(lengths.tolist()), block_size=16, heads=heads,
+                         kv_heads=kv_heads, seed=batch)
+    dev = to_dev(args)
+    print(f"paired units B={batch} {heads}/{kv_heads}", flush=True)
+    actual = paged_attention(*dev, backend="hip")
+    assert max_err(actual, oracle(args)) <= GATE[torch.bfloat16]
+    for b in (0, 1, batch // 2, batch - 1):
+        alone = paged_attention(dev[0][b:b + 1], dev[1], dev[2], dev[3][b:b + 1], dev[4][b:b + 1], 16,
+                                backend="hip")
+        assert (alone.float() - actual[b:b + 1].float()).abs().max().item() <= GATE[torch.bfloat16]
+
+
 @pytest.mark.parametrize("partition", [64, 128, 256, 512, 4096])
 def test_split_count_does_not_change_result(partition):
     """Split-K invariant: any partition size gives the single-partition answer."""
