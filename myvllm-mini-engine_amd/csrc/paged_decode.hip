@@ -149,7 +149,7 @@ struct DecodePlan {
     int partition;
     int max_parts;
     int gtile;  // G of the kernel instance
-    int waves;  // waves per work-group (kSplitWaves, kWholeWaves or kLongWaves)
+    int waves;  // waves per work-group (kSplitWaves or kWholeWaves; kFlatWaves in the walk)
     bool stream;  // non-temporal K/V loads
     int flat_groups;  // > 0: balanced walk with this many work-groups
 };
@@ -182,13 +182,15 @@ constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 // capacity only).  Enough (sequence, kv head) units to occupy every CU, a
 // capacity of one 16-wave step, or two steps with more than a quarter of the
 // CUs' worth of units: one work-group per unit over the whole context, merged
-// in LDS (8 waves, 16 for units of at least kLongUnitBytes unless two 8-wave
-// work-groups per CU hold every unit, which then pair long sequences with
-// short ones; below two 16-wave steps 8, or 4 with more units than CUs), or,
-// for one round of long units, the balanced walk.  Otherwise split-K into partitions of 4-wave
-// work-groups, sized to give every CU about two work-groups (at least one
-// 4-wave step each), plus a merge kernel.  `requested` > 0 forces split-K with
-// that partition length (rounded to the wave tiling), -1 the balanced walk.
+// in LDS (8 waves; with two work-groups per CU holding every unit, long
+// sequences paired with short ones; below two 16-wave steps, 4 waves when
+// the units outnumber the CUs), or, for one round of long units
+// (kLongUnitBytes), the balanced walk.  (A "16-wave step" is 16 wave
+// iterations of tokens, the unit the thresholds were measured in.)
+// Otherwise split-K into partitions of 4-wave work-groups, sized to give
+// every CU about two work-groups (at least one 4-wave step each), plus a
+// merge kernel.  `requested` > 0 forces split-K with that partition length
+// (rounded to the wave tiling), -1 the balanced walk.
 //
 // Measured at head_dim 128 (bf16, block 16, 16/8 heads, µs per call in a
 // graph): whole-sequence against split-K at 64/128/256 keys.
@@ -220,14 +222,7 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
         // B4 / ctx 256 6.82 -> 6.00, B32 / ctx 256 bf16 8.76 -> 7.32; but
         // B64 / ctx 128 7.18 -> 7.39 (512 units), hence 4 there.
         const int short_waves = units <= kDeviceCUs ? kWholeWaves : kSplitWaves;
-        // Long units keep 16 waves, except when two 8-wave work-groups per
-        // CU hold every unit at once (units in (CUs, 2 CUs]): the launch
-        // then pairs each long sequence with a short one (lpt_pair).  64
-        // sequences of contexts U[1,4096] sharing a 1024-token prefix (bf16,
-        // block 16): 88.0 -> 81.1 µs; U[1,4096] fp16 block 256: 81.7 -> 77.9.
-        const bool two_per_cu = units > kDeviceCUs && units <= 2 * kDeviceCUs;
-        p.waves = cap < 2 * whole_step ? short_waves
-                  : cap * head_dim * 4 >= kLongUnitBytes && !two_per_cu ? kLongWaves : kWholeWaves;
+        p.waves = cap < 2 * whole_step ? short_waves : kWholeWaves;
         part = (cap + tile - 1) / tile * tile;
     } else {
         p.waves = kSplitWaves;
@@ -243,8 +238,9 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     }
     p.partition = (int)part;
     p.max_parts = (int)((cap + part - 1) / part);
-    // One round of long units (at most one per CU, each of the 16-wave
-    // regime), or a request (requested == -1), takes the balanced walk:
+    // One round of long units (at most one per CU, each holding
+    // kLongUnitBytes of K+V or more), or a request (requested == -1), takes
+    // the balanced walk:
     // there, one work-group per unit leaves the CUs holding the shortest
     // units idle while the longest stream alone, whatever the order.  32
     // sequences of contexts U[1,4096] (fp16, block 256): 70.5 -> 62.5 µs per
@@ -252,9 +248,9 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     // longest-first order already balances the CUs, and the walk was slower
     // (64 sequences U[1,4096] sharing a 1024-token prefix, bf16, block 16:
     // 88.1 -> 90.5 µs; 128 sequences U[1,4096]: 166.4 -> 169.2).
+    const bool long_units = (double)cap * (double)head_dim * 4.0 >= (double)kLongUnitBytes;
     const bool flat = batch <= kLptMax &&
-                      (requested == -1 ||
-                       (requested <= 0 && whole && p.waves == kLongWaves && units <= kDeviceCUs));
+                      (requested == -1 || (requested <= 0 && whole && long_units && units <= kDeviceCUs));
     if (flat) {
         p.flat_groups = kFlatGroups;
         p.waves = kFlatWaves;
@@ -290,8 +286,7 @@ void launch_decode_nw(const DecodeArgs& a, int units, bool page_uniform, bool st
 
 template <typename T, int D, int G>
 void launch_decode(const DecodeArgs& a, const DecodePlan& p, int units, bool page_uniform, hipStream_t s) {
-    if (p.waves == kLongWaves) launch_decode_nw<T, D, G, kLongWaves>(a, units, page_uniform, p.stream, s);
-    else if (p.waves == kWholeWaves) launch_decode_nw<T, D, G, kWholeWaves>(a, units, page_uniform, p.stream, s);
+    if (p.waves == kWholeWaves) launch_decode_nw<T, D, G, kWholeWaves>(a, units, page_uniform, p.stream, s);
     else launch_decode_nw<T, D, G, kSplitWaves>(a, units, page_uniform, p.stream, s);
     if (a.flat_groups > 0)
         hipLaunchKernelGGL((paged_decode_flat_merge_kernel<T, D, G>), dim3(a.flat_groups), dim3(kLptMax), 0, s, a);

@@ -18,9 +18,7 @@ void launch_decode_fused(const DecodeArgs& a, dim3 grid, bool page_uniform, hipS
     MVME_FUSED_NW_S(T, D, G, kSplitWaves, false)      \
     MVME_FUSED_NW_S(T, D, G, kSplitWaves, true)       \
     MVME_FUSED_NW_S(T, D, G, kWholeWaves, false)      \
-    MVME_FUSED_NW_S(T, D, G, kWholeWaves, true)       \
-    MVME_FUSED_NW_S(T, D, G, kLongWaves, false)       \
-    MVME_FUSED_NW_S(T, D, G, kLongWaves, true)
+    MVME_FUSED_NW_S(T, D, G, kWholeWaves, true)
 #define MVME_FUSED_D(T, D) MVME_FUSED_G(T, D, 1) MVME_FUSED_G(T, D, 2) MVME_FUSED_G(T, D, 4)
 #define MVME_FUSED_T(T) MVME_FUSED_D(T, 16) MVME_FUSED_D(T, 32) MVME_FUSED_D(T, 64) MVME_FUSED_D(T, 128) \
     MVME_FUSED_D(T, 256)

@@ -42,16 +42,17 @@
 namespace mvme {
 
 constexpr int kSplitWaves = 4;   // waves per work-group in split-K mode
-// Waves per work-group covering a whole sequence: 8, or 16 when one unit's
-// capacity holds kLongUnitBytes of K+V or more.  Uniform decode at head_dim
-// 128 (fp16, block 256, us per call): B32/ctx2048 43.7 at 16 waves, 42.9 at
-// 8 (45.2 at 12); B128/ctx1024 91.4 -> 83.9; B64/ctx2048 83.8 -> 83.3; but
-// B32/ctx4096 84.4 -> 85.3, and the ragged B64 case (contexts up to 4096,
-// block 16) 86.6 -> 91.1, where the longest units' work-groups finish last
-// and stream faster with more waves in flight.  A plain streaming read of a
-// 256 MiB layer likewise peaks at 8 waves per CU (6.8 TB/s; 16 waves 6.4).
+// Waves per work-group covering a whole sequence.  Uniform decode at head_dim
+// 128 (fp16, block 256, us per call), 16 waves against 8: B32/ctx2048 43.7 ->
+// 42.9 (45.2 at 12); B128/ctx1024 91.4 -> 83.9; B64/ctx2048 83.8 -> 83.3.  A
+// plain streaming read of a 256 MiB layer likewise peaks at 8 waves per CU
+// (6.8 TB/s; 16 waves 6.4).  Long units (kLongUnitBytes of K+V or more) once
+// took 16 waves, which were ahead only where 8-wave work-groups sat badly
+// paired on the CUs or a round of units was unbalanced; the paired order and
+// the balanced walk now serve those shapes (ragged B64 / ctx 4096, block 16:
+// 88.0 at 16 -> 81.1; ragged B128 165.8 -> 161.3; ragged B256 349.5 ->
+// 333.1; uniform B128 / ctx 4096 328.8 -> 327.1).
 constexpr int kWholeWaves = 8;
-constexpr int kLongWaves = 16;
 constexpr int64_t kLongUnitBytes = int64_t(2) << 20;
 constexpr int kLptMax = 256;     // largest batch whose units go longest context first
 static_assert(kSplitWaves * kWave >= kLptMax, "one thread per sequence key");
