@@ -6,8 +6,8 @@
 // (sequence, kv head, G-query-head tile, partition of `partition` tokens).
 // All G query heads that share a kv head are served by the same loads, so
 // every K/V byte of a partition is fetched from HBM exactly once.  When the
-// (sequence, kv head) units alone fill the GPU, one work-group (4, 8 or 16
-// waves by the context's length) covers a whole sequence and merges its waves
+// (sequence, kv head) units alone fill the GPU, one work-group (4 or 8 waves
+// by the context's length) covers a whole sequence and merges its waves
 // in LDS: one kernel, no workspace.
 // Otherwise the context is split into partitions of 4-wave work-groups
 // (split-K) whose fp32 partials a second, small kernel merges.  A third
