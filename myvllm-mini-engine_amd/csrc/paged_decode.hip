@@ -216,9 +216,9 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     const bool whole = units >= kDeviceCUs - kDeviceCUs / 16 || cap <= whole_step ||
                        (cap <= 2 * whole_step && units > kDeviceCUs / 4);
     if (requested <= 0 && whole) {
-        // Below two 16-wave steps: 8 waves (a 128-token context in one
-        // iteration of loads) while the units fit the CUs, 4 beyond (more
-        // work-groups per CU).  µs per call: B1 / ctx 128 fp16 4.85 -> 4.77,
+        // Below two whole steps (512 tokens at D=128): 8 waves (a 128-token
+        // context in one iteration of loads) while the units fit the CUs, 4
+        // beyond (more work-groups per CU).  µs per call: B1 / ctx 128 fp16 4.85 -> 4.77,
         // B4 / ctx 256 6.82 -> 6.00, B32 / ctx 256 bf16 8.76 -> 7.32; but
         // B64 / ctx 128 7.18 -> 7.39 (512 units), hence 4 there.
         const int short_waves = units <= kDeviceCUs ? kWholeWaves : kSplitWaves;
