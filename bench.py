@@ -498,8 +498,8 @@ def _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra):
         "GBps_logical": logical / per_call / 1e9, "unique_rows": c["unique_rows"], "logical_rows": c["logical_rows"],
         "max_abs_error": err}
     del c, out
-    # Ragged B=32, ctx U[1,4096], fp16, block 256: one unit per CU, each of
-    # the 16-wave regime, so the plan takes the balanced walk.
+    # Ragged B=32, ctx U[1,4096], fp16, block 256: one unit per CU, each with
+    # 2 MiB of K+V capacity, so the plan takes the balanced walk.
     r = workloads.ragged_decode_case(device=dev)
     rout = torch.empty_like(r["query"])
     fnr = lambda: paged_attention(r["query"], r["key_cache"], r["value_cache"], r["block_tables"],  # noqa: E731
