@@ -119,10 +119,11 @@ int mvme_gather_kv_cache(void* key_out, void* value_out,
  * Bytes of device workspace mvme_paged_attention needs for these shapes
  * (0 when no split-K merge is required).  Pure host function.
  * partition_tokens: 0 selects the library's plan; > 0 forces split-K
- * partitions of that many tokens; -1 forces the balanced walk (batch <= 256:
- * every (sequence, kv head) unit laid end to end and cut into equal shares of
- * tokens, one per work-group, the units cut by a share boundary merged from
- * their pieces).
+ * partitions of that many tokens; -1 forces the balanced walk when batch <=
+ * 256 (every (sequence, kv head) unit laid end to end and cut into equal
+ * shares of tokens, one per work-group, the units cut by a share boundary
+ * merged from their pieces); larger batches, and other negative values,
+ * take the library's plan.
  */
 size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_heads, int64_t kv_heads,
                                            int64_t head_dim, int64_t block_size,

@@ -75,7 +75,8 @@ def paged_attention(query, key_cache, value_cache, block_tables, context_lens, b
     context_lens [B] int64.  Returns [B, Hq, D] in the query dtype.
 
     ``partition_tokens`` (0 = library plan) sets the split-K partition, or
-    with -1 forces the balanced walk (equal shares of tokens per work-group);
+    with -1 forces the balanced walk (equal shares of tokens per work-group;
+    batches above 256 take the plan);
     ``out`` / ``workspace`` let a caller supply preallocated buffers.
     """
     if backend != "hip":
