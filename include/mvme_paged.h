@@ -137,7 +137,8 @@ size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_heads, int64
  * Sequences with context_lens[b] <= 0 or beyond the table capacity produce
  * zeros; out-of-range pages are skipped.  fp32 accumulation, fp32 split-K
  * merge.  `workspace` must hold mvme_paged_attention_workspace_size(...)
- * bytes (may be NULL when that is 0); partition_tokens as there.
+ * bytes (may be NULL when that is 0), 16-byte aligned when the call takes
+ * the balanced walk; partition_tokens as there.
  * Replaces: paged_attention_cuda, attention_vector128, attention_partition
  *   and merge_partitions (mini_engine/kernels/csrc/paged_attention.cu:52-280),
  *   bound as extension.paged_attention (csrc/bindings.cpp:152-184, :196-199)

@@ -89,58 +89,89 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeArgs a) {
     if (owns_dim) static_cast<uint16_t*>(a.out)[bh * D + tid] = T::from_float(sum > 0.f ? o / sum : 0.f);
 }
 
-// Merge of the balanced walk: work-group l merges the unit whose last chunk
-// lies in share l when that unit began in an earlier share.  The unit's
-// pieces are the shares from the one holding its first chunk up to l; the
-// first of them wrote its piece as its share's last segment (row slot 1)
-// unless the share began with the unit, every later one as its share's first
-// segment (slot 0).  Shares left empty (fewer chunks than work-groups) wrote
-// nothing and are skipped.
+// Merge of the balanced walk: work-group l merges the unit its share's
+// descriptor names (one that began in an earlier share and ends in this
+// one).  The unit's pieces are the shares from p0, the one holding its first
+// chunk, up to l; share p0 wrote its piece in row slot `slot0` (1 when the
+// unit was its last segment), every later one as its first segment (slot 0).
+// Shares left empty (fewer chunks than work-groups) wrote nothing: they get
+// weight 0 and read the merging share's own row instead, so every load is
+// unconditional.  A unit has at most one piece per work-group of the walk:
+// thread t reads piece t's (reference, sum) pairs, the block maximum gives
+// the reference, and the weights and row offsets go to LDS; each output dim
+// then sums its pieces in order, kBatch loads at a time (the same sums, in
+// the same order, as one piece after the other; a zero weight adds nothing).
+// Work-group g merges share (g mod 8) * kFlatGroups/8 + g/8, the share the
+// attention kernel's work-group g computed, so the merge runs on the XCD
+// whose L2 holds that share's partials.  Measured against the first version
+// (one piece after the other, each a dependent load, and the walk's prefix
+// sums recomputed before the first load; µs per call): one sequence of
+// 32768 keys 32.0 -> 29.7, two of 8192 27.5 -> 18.3, 8 of 512 11.9 -> 9.6.
 template <typename T, int D, int G>
 __global__ __launch_bounds__(kLptMax) void paged_decode_flat_merge_kernel(DecodeArgs a) {
-    __shared__ int fl_len[kLptMax];
-    __shared__ int fl_pref[kLptMax + 1];
-    __shared__ int fl_tot[kLptMax / kWave];
-    flat_prefix(a, DecodeShape<D>::kTpi, fl_len, fl_pref, fl_tot);
-    const int ng = a.flat_groups;
-    const int64_t l = blockIdx.x;
-    const int per_seq = a.kv_heads * a.gtiles;
-    const int64_t wc = fl_pref[a.batch];
-    const int64_t total = wc * per_seq;
-    const int64_t s0 = flat_share_start(l, total, ng);
-    const int64_t s1 = flat_share_start(l + 1, total, ng);
-    if (s0 >= s1) return;
-    const int r = (int)(s0 / wc);
-    const int b = flat_seq_of(fl_pref, a.batch, s0 - r * wc);
-    const int64_t first = r * wc + fl_pref[b];
-    const int64_t last = r * wc + fl_pref[b + 1];
-    if (first == s0 || last > s1) return;  // not cut, or its last piece is later
-    const int64_t p0 = ((first + 1) * ng - 1) / total;  // share holding chunk `first`
-    const int kvh = r / a.gtiles;
-    const int h0 = kvh * a.group + (r - kvh * a.gtiles) * G;
-    auto row_of = [&](int64_t p, int g) __attribute__((always_inline)) -> int64_t {
-        const int slot = p == p0 && flat_share_start(p, total, ng) < first ? 1 : 0;
-        return (p * 2 + slot) * G + g;
-    };
-    auto empty = [&](int64_t p) __attribute__((always_inline)) {
-        return flat_share_start(p, total, ng) == flat_share_start(p + 1, total, ng);
-    };
-    for (int idx = threadIdx.x; idx < G * D; idx += kLptMax) {
+    __shared__ float sm_red[G][kLptMax / kWave];
+    __shared__ float sm_w[G][kLptMax];
+    __shared__ float sm_lw[G][kLptMax];
+    __shared__ int64_t sm_row[kLptMax];
+    const int64_t l = (blockIdx.x & 7) * (kFlatGroups >> 3) + (blockIdx.x >> 3);
+    const FlatMergeDesc dsc = a.ws_flat[l];
+    if (dsc.b < 0) return;
+    const int64_t total = dsc.total;
+    const int64_t p0 = dsc.p0;
+    const int n = (int)(l - p0 + 1);
+    const int kvh = dsc.r / a.gtiles;
+    const int h0 = kvh * a.group + (dsc.r - kvh * a.gtiles) * G;
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+    const int64_t p = p0 + tid;
+    const bool live = tid < n && flat_share_start(p, total) < flat_share_start(p + 1, total);
+    const int64_t row = (p * 2 + (tid == 0 ? dsc.slot0 : 0)) * G;
+    float m[G], lsum[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m[g] = live ? a.ws_ml[(row + g) * 2] : kNegInf;
+        lsum[g] = live ? a.ws_ml[(row + g) * 2 + 1] : 0.f;
+        float v = m[g];
+#pragma unroll
+        for (int off = kWave / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+        if (lane == 0) sm_red[g][wave] = v;
+    }
+    // Empty pieces read the merging share's own row (always written) and
+    // are dropped by their zero weight.
+    if (tid < n) sm_row[tid] = live ? row : (l * 2) * G;
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float mx = sm_red[g][0];
+#pragma unroll
+        for (int w = 1; w < kLptMax / kWave; ++w) mx = fmaxf(mx, sm_red[g][w]);
+        const float ref = mx == kNegInf ? 0.f : mx;
+        const float w = live ? fast_exp2(m[g] - ref) : 0.f;
+        if (tid < n) {
+            sm_w[g][tid] = w;
+            sm_lw[g][tid] = live ? lsum[g] * w : 0.f;
+        }
+    }
+    __syncthreads();
+    constexpr int kBatch = 16;
+    for (int idx = tid; idx < G * D; idx += kLptMax) {
         const int g = idx / D;
         const int d = idx - g * D;
-        float mx = kNegInf;
-        for (int64_t p = p0; p <= l; ++p)
-            if (!empty(p)) mx = fmaxf(mx, a.ws_ml[row_of(p, g) * 2]);
-        const float ref = mx == kNegInf ? 0.f : mx;
         float sum = 0.f, o = 0.f;
-        for (int64_t p = p0; p <= l; ++p) {
-            if (empty(p)) continue;
-            const int64_t row = row_of(p, g);
-            const float w = fast_exp2(a.ws_ml[row * 2] - ref);
-            sum += a.ws_ml[row * 2 + 1] * w;
-            o += a.ws_acc[row * D + d] * w;
+        for (int t0 = 0; t0 < n; t0 += kBatch) {
+            float av[kBatch];
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                av[k] = a.ws_acc[(sm_row[min(t0 + k, n - 1)] + g) * D + d];
+            }
+#pragma unroll
+            for (int k = 0; k < kBatch; ++k) {
+                const int t = min(t0 + k, n - 1);
+                const bool use = t0 + k < n && sm_w[g][t] != 0.f;
+                sum += use ? sm_lw[g][t] : 0.f;
+                o += use ? av[k] * sm_w[g][t] : 0.f;
+            }
         }
-        static_cast<uint16_t*>(a.out)[((int64_t)b * a.q_heads + h0 + g) * D + d] =
+        static_cast<uint16_t*>(a.out)[((int64_t)dsc.b * a.q_heads + h0 + g) * D + d] =
             T::from_float(sum > 0.f ? o / sum : 0.f);
     }
 }
@@ -154,11 +185,6 @@ struct DecodePlan {
     int flat_groups;  // > 0: balanced walk with this many work-groups
 };
 
-// Balanced walk: work-groups (a multiple of 8, the XCD count; kFlatWaves
-// waves each).  Measured on 32 sequences of contexts U[1,4096] (fp16, block
-// 256, µs per call): 256 x 8 waves 62.5, 256 x 16 63.3, 512 x 8 63.3,
-// 1024 x 4 67.9.
-constexpr int kFlatGroups = 256;
 
 constexpr int64_t kStreamBytes = int64_t(64) << 20;  // K+V bytes within capacity above which loads stream
 
@@ -238,19 +264,25 @@ DecodePlan make_decode_plan(int64_t batch, int64_t q_heads, int64_t kv_heads, in
     }
     p.partition = (int)part;
     p.max_parts = (int)((cap + part - 1) / part);
-    // One round of long units (at most one per CU, each holding
-    // kLongUnitBytes of K+V or more), or a request (requested == -1), takes
-    // the balanced walk:
-    // there, one work-group per unit leaves the CUs holding the shortest
-    // units idle while the longest stream alone, whatever the order.  32
-    // sequences of contexts U[1,4096] (fp16, block 256): 70.5 -> 62.5 µs per
-    // call; all 4096 tokens: 84.3 -> 84.6.  With two or more units per CU the
+    // Long units (kLongUnitBytes of K+V capacity or more) numbering at most
+    // one per CU, or a request (requested == -1), take the balanced walk.
+    // With one work-group per unit the CUs holding the shortest units idle
+    // while the longest stream alone, whatever the order: 32 sequences of
+    // contexts U[1,4096] (fp16, block 256) 70.5 -> 62.5 µs per call, all 4096
+    // tokens 84.3 -> 84.6.  Fewer units, which split-K cuts into partitions
+    // sized by capacity, leave ragged batches with empty partitions and
+    // uneven CUs (bf16, block 16 unless noted, µs per call, split-K ->
+    // walk): 24 sequences U[1,4096] 60.8 -> 47.3, 16 U[1,8192] 58.1 -> 46.4,
+    // 8 U[1,8192] fp16 block 256 30.1 -> 27.4, 4 U[1,32768] block 256 61.5
+    // -> 56.9; equal lengths cost the walk 2-6 % (8 x 4096 26.2 -> 27.7, 1 x
+    // 32768 block 256 28.5 -> 29.7) and short capacities more (8 x 512 8.4
+    // -> 9.6), so those keep split-K.  With two or more units per CU the
     // longest-first order already balances the CUs, and the walk was slower
     // (64 sequences U[1,4096] sharing a 1024-token prefix, bf16, block 16:
     // 88.1 -> 90.5 µs; 128 sequences U[1,4096]: 166.4 -> 169.2).
     const bool long_units = (double)cap * (double)head_dim * 4.0 >= (double)kLongUnitBytes;
     const bool flat = batch <= kLptMax &&
-                      (requested == -1 || (requested <= 0 && whole && long_units && units <= kDeviceCUs));
+                      (requested == -1 || (requested <= 0 && long_units && units <= kDeviceCUs));
     if (flat) {
         p.flat_groups = kFlatGroups;
         p.waves = kFlatWaves;
@@ -355,7 +387,9 @@ extern "C" size_t mvme_paged_attention_workspace_size(int64_t batch, int64_t q_h
         return 0;
     const DecodePlan p = make_decode_plan(batch, q_heads, kv_heads, head_dim, block_size, table_width,
                                           partition_tokens);
-    if (p.flat_groups > 0) return (size_t)p.flat_groups * 2 * p.gtile * (head_dim + 2) * sizeof(float);
+    if (p.flat_groups > 0)
+        return (size_t)p.flat_groups * 2 * p.gtile * (head_dim + 2) * sizeof(float) +
+               (size_t)p.flat_groups * sizeof(FlatMergeDesc);
     if (p.max_parts <= 1) return 0;
     return (size_t)batch * q_heads * p.max_parts * (head_dim + 2) * sizeof(float);
 }
@@ -399,6 +433,13 @@ int launch_paged_attention(void* out, const void* query, const void* key_cache, 
         a.ws_acc = static_cast<float*>(workspace);
         a.ws_ml = a.ws_acc + (p.flat_groups > 0 ? (int64_t)p.flat_groups * 2 * p.gtile
                                                  : batch * q_heads * p.max_parts) * head_dim;
+        // After the partial rows (a multiple of 16 bytes: 256 shares x 2 x G
+        // x (D + 2) floats).
+        if (p.flat_groups > 0) {
+            if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+                return fail(MVME_EINVAL, "the balanced walk needs a 16-byte aligned workspace");
+            a.ws_flat = reinterpret_cast<FlatMergeDesc*>(a.ws_ml + (int64_t)p.flat_groups * 2 * p.gtile * 2);
+        }
     }
     a.q_heads = (int)q_heads;
     a.kv_heads = (int)kv_heads;

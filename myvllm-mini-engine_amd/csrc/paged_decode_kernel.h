@@ -70,6 +70,19 @@ struct DecodeShape {
     static constexpr int kTpi = kTpl * kDecodeLoads;   // tokens per wave iteration
 };
 
+// Balanced walk: the merge duty of share l, written by the attention
+// kernel's work-group for that share on every call and read by the merge
+// kernel's work-group l.  A share merges the unit it began with when that
+// unit started in an earlier share and ends inside this one.
+struct FlatMergeDesc {
+    int b;          // the unit's sequence, -1 when the share merges nothing
+    int r;          // the unit's column (kv head * gtiles + query-head tile)
+    int p0;         // share holding the unit's first piece
+    int slot0;      // row slot of that piece (1: its share's last segment)
+    int64_t total;  // chunks of the call, for the empty-share test
+    int64_t pad;
+};
+
 struct DecodeArgs {
     void* out;
     const void* query;
@@ -79,6 +92,7 @@ struct DecodeArgs {
     const int64_t* lens;
     float* ws_acc;  // [batch*q_heads, max_parts, D]
     float* ws_ml;   // [batch*q_heads, max_parts, 2]  (max in log2 units, sum)
+    FlatMergeDesc* ws_flat;  // balanced walk: [flat_groups] merge duties
     int q_heads;
     int kv_heads;
     int group;      // q_heads / kv_heads
@@ -96,7 +110,8 @@ struct DecodeArgs {
     // that each CU pairs a long sequence with a short one.
     int lpt_pair;
     // Balanced walk (flat_groups > 0, batch <= kLptMax): `flat_groups`
-    // work-groups, each taking an equal share of the call's token chunks.
+    // (kFlatGroups) work-groups, each taking an equal share of the call's
+    // token chunks.
     int flat_groups;
     int batch;
     float scale_log2;
@@ -184,8 +199,16 @@ __device__ inline int flat_seq_of(const int* pref, int n, int64_t cin) {
     return count;
 }
 
+// Work-groups of the walk: a multiple of 8, the XCD count, kFlatWaves waves
+// each, and a power of two (share bounds are a shift).  Measured on 32
+// sequences of contexts U[1,4096] (fp16, block 256, µs per call): 256 x 8
+// waves 62.5, 256 x 16 63.3, 512 x 8 63.3, 1024 x 4 67.9.
+constexpr int kFlatShift = 8;
+constexpr int kFlatGroups = 1 << kFlatShift;
+static_assert(kFlatGroups <= kLptMax, "one merge thread per piece");
+
 // First chunk of logical work-group l's share.
-__device__ inline int64_t flat_share_start(int64_t l, int64_t total, int groups) { return l * total / groups; }
+__device__ inline int64_t flat_share_start(int64_t l, int64_t total) { return (l * total) >> kFlatShift; }
 
 // PRO: the kernel runs the fused prologue (a.prologue 1 or 2); without it
 // the prologue's code is not compiled in.  FLAT: the balanced walk (its
@@ -216,7 +239,7 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
     int64_t fl_wc = 0, fl_pos = 0, fl_stop = 0, fl_row = 0, fl_row_later = 0;
     if constexpr (FLAT) {
         flat_prefix(a, S::kTpi, fl_len, fl_pref, fl_tot);
-        const int ng = a.flat_groups;
+        constexpr int ng = kFlatGroups;
         // Work-groups go to the 8 XCDs round robin; consecutive shares run
         // on one XCD, so a column's rows (and the pages its sequences
         // share) meet in one L2.
@@ -226,11 +249,29 @@ __global__ __launch_bounds__(NW * kWave) void paged_decode_kernel(DecodeArgs a) 
         // modes).
         fl_wc = __builtin_amdgcn_readfirstlane(fl_pref[a.batch]);
         const int64_t total = fl_wc * per_seq;
-        fl_pos = flat_share_start(l, total, ng);
-        fl_stop = flat_share_start(l + 1, total, ng);
-        if (fl_pos >= fl_stop) return;
+        fl_pos = flat_share_start(l, total);
+        fl_stop = flat_share_start(l + 1, total);
+        if (fl_pos >= fl_stop) {
+            if (threadIdx.x == 0) a.ws_flat[l] = FlatMergeDesc{-1, 0, 0, 0, total, 0};
+            return;
+        }
         r = (int)(fl_pos / fl_wc);
         b = flat_seq_of(fl_pref, a.batch, fl_pos - r * fl_wc);
+        if (threadIdx.x == 0) {
+            // The unit this share begins with: merged here when it began in
+            // an earlier share and ends in this one.
+            const int64_t first = (int64_t)r * fl_wc + fl_pref[b];
+            const int64_t last = (int64_t)r * fl_wc + fl_pref[b + 1];
+            FlatMergeDesc d{-1, 0, 0, 0, total, 0};
+            if (first < fl_pos && last <= fl_stop) {
+                const int64_t p0 = ((first + 1) * ng - 1) / total;  // share holding chunk `first`
+                d.b = b;
+                d.r = r;
+                d.p0 = (int)p0;
+                d.slot0 = flat_share_start(p0, total) < first ? 1 : 0;
+            }
+            a.ws_flat[l] = d;
+        }
         // Partial rows: the share's first segment, then its last.
         fl_row = (int64_t)l * 2 * G;
         fl_row_later = fl_row + G;

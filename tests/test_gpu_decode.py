@@ -135,19 +135,21 @@ def ragged_lengths(batch, high, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("dim,heads,kv_heads,lengths,block_size", [
-    (128, 16, 8, ragged_lengths(32, 4096, 1), 16),    # the plan's own pick (256 long units)
-    (128, 16, 8, (1, 5), 16),                        # fewer chunks than work-groups: empty shares
-    (64, 16, 4, ragged_lengths(256, 600, 2), 16),    # 256 sequences, 4-head tiles
-    (256, 8, 8, (3000, 17, 1, 4096, 900), 32),       # group 1, head dim 256
-    (80, 12, 4, (100, 2000, 3), 7),                  # group 3, pages not a multiple of the wave tile
-    (16, 32, 8, ragged_lengths(9, 5000, 3), 64),     # head dim 16: 128-token chunks
+@pytest.mark.parametrize("dim,heads,kv_heads,lengths,block_size,plan", [
+    (128, 16, 8, ragged_lengths(32, 4096, 1), 16, True),   # the plan's pick: 256 long units
+    (128, 16, 8, (1, 5), 16, False),                       # fewer chunks than work-groups: empty shares
+    (64, 16, 4, ragged_lengths(256, 600, 2), 16, False),   # 256 sequences, 4-head tiles
+    (256, 8, 8, (3000, 17, 1, 4096, 900), 32, True),       # group 1, head dim 256 (40 long units)
+    (80, 12, 4, (100, 2000, 3), 7, False),                 # group 3, pages not a multiple of the wave tile
+    (16, 32, 8, ragged_lengths(9, 5000, 3), 64, False),    # head dim 16: 128-token chunks
+    (128, 16, 8, ragged_lengths(16, 8192, 4), 16, True),   # the plan's pick: 128 long units
+    (128, 2, 1, (20000,), 16, True),                       # one unit over every share: 256 pieces
 ])
-def test_balanced_walk_matches_oracle(dtype, dim, heads, kv_heads, lengths, block_size):
+def test_balanced_walk_matches_oracle(dtype, dim, heads, kv_heads, lengths, block_size, plan):
     """Balanced walk: units laid end to end and cut into equal shares per
     work-group; units cut by a share boundary are merged from their pieces.
-    Forced with partition_tokens=-1; the 32-sequence case also takes it by
-    the library's plan."""
+    Forced with partition_tokens=-1; the plan takes it too for long units
+    (2 MiB of K+V capacity or more) numbering at most one per CU."""
     args = decode_inputs(dtype, head_dim=dim, heads=heads, kv_heads=kv_heads, lengths=lengths,
                          block_size=block_size, seed=len(lengths) + dim)
     dev = to_dev(args)
@@ -157,7 +159,7 @@ def test_balanced_walk_matches_oracle(dtype, dim, heads, kv_heads, lengths, bloc
     assert max_err(walk, expected) <= GATE[dtype]
     single = paged_attention(*dev, backend="hip", partition_tokens=1 << 20)
     assert (walk.float() - single.float()).abs().max().item() <= GATE[dtype]
-    if len(lengths) == 32:
+    if plan:
         assert torch.equal(paged_attention(*dev, backend="hip"), walk)
 
 
@@ -177,17 +179,19 @@ def test_balanced_walk_trusted_empty_and_invalid_rows():
     assert (actual[0].float() - alone[0].float()).abs().max().item() <= GATE[torch.bfloat16]
 
 
-@pytest.mark.parametrize("batch,block_size,low,high", [(2, 256, 40000, 40001), (40, 16, 1500, 2600)])
-def test_streaming_loads_match_oracle(batch, block_size, low, high):
+@pytest.mark.parametrize("batch,block_size,low,high,partition", [
+    (2, 256, 40000, 40001, 4096), (2, 256, 40000, 40001, 0), (40, 16, 1500, 2600, 0)])
+def test_streaming_loads_match_oracle(batch, block_size, low, high, partition):
     """Calls with more than 64 MiB of K/V within the tables' capacity load
-    rows with the non-temporal hint: split-K for two long sequences,
-    whole-sequence work-groups for forty ragged ones."""
+    rows with the non-temporal hint: split-K (forced) and the balanced walk
+    (the plan's choice) for two long sequences, whole-sequence work-groups
+    for forty ragged ones."""
     gen = torch.Generator().manual_seed(batch)
     lengths = tuple(torch.randint(low, high, (batch,), generator=gen).tolist())
     args = decode_inputs(torch.float16, lengths=lengths, block_size=block_size, seed=batch)
     width = args[3].shape[1]
     assert batch * width * block_size * 8 * 128 * 4 > 64 << 20
-    actual = paged_attention(*to_dev(args), backend="hip")
+    actual = paged_attention(*to_dev(args), backend="hip", partition_tokens=partition)
     assert max_err(actual, oracle(args)) <= GATE[torch.float16]
 
 
