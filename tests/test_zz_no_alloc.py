@@ -73,3 +73,14 @@ def test_noalloc_whole_sequence_and_rejection():
                  4096, 16, ext.FP16, ext.current_stream(q.device))
     torch.cuda.synchronize()
     assert not out.any()
+
+
+def test_noalloc_balanced_walk_two_calls():
+    """The balanced walk in the scratch (partial rows and the per-share merge
+    descriptors): the plan's pick for long units, then a smaller forced walk
+    that rewrites every descriptor."""
+    print("no-alloc decode: balanced walk, long units then a forced small call", flush=True)
+    long_units = decode_inputs(torch.bfloat16, lengths=(5000, 17, 4100), block_size=16, seed=74)
+    small = decode_inputs(torch.bfloat16, lengths=(700,), block_size=32, seed=72)
+    assert check(long_units) > 0
+    assert check(small, partition=-1) > 0
