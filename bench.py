@@ -519,6 +519,32 @@ def _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra):
         "us_per_call": per_call * 1e6, "GBps": nbytes / per_call / 1e9,
         "frac_of_hbm_peak": nbytes / per_call / 1e9 / HBM_PEAK_GBS, "rows": rows, "algorithmic_bytes": nbytes,
         "max_abs_error": err}
+    del r, rout
+    # Ragged B=16, ctx U[1,8192], bf16, block 16: 128 long units on 256 CUs.
+    # The plan takes the balanced walk; split-K with the partitions sized
+    # from the capacity (2048 tokens: two work-groups per CU) is timed beside it.
+    w = workloads.ragged_decode_case(device=dev, batch=16, max_len=8192, block_size=16, dtype=torch.bfloat16,
+                                     seed=BASE_SEED + 6)
+    wout = torch.empty_like(w["query"])
+    ws_w = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+
+    def timed(partition):
+        def run():
+            for _ in range(10):
+                paged_attention(w["query"], w["key_cache"], w["value_cache"], w["block_tables"], w["context_lens"],
+                                16, backend="hip", validate=False, partition_tokens=partition, out=wout,
+                                workspace=ws_w)
+        ms, _ = graph_time_ms(run, torch, calls_per_graph=10, replays=10, warmup=2)
+        return ms / 10 * 1e-3
+    split_call = timed(2048)
+    walk_call = timed(0)
+    rows = int(w["context_lens"].sum())
+    nbytes = rows * 4096 + 2 * 16 * 16 * 128 * 2 + 16 * 512 * 8 + 16 * 8
+    err = None if cpu is None else max_abs(wout, cpu.decode({k: w[k].cpu() for k in DECODE_NAMES}, 16))
+    extra["ragged_b16_ctx8192_bf16_balanced_walk"] = {
+        "us_per_call": walk_call * 1e6, "GBps": nbytes / walk_call / 1e9,
+        "frac_of_hbm_peak": nbytes / walk_call / 1e9 / HBM_PEAK_GBS, "split_k_2048_us_per_call": split_call * 1e6,
+        "rows": rows, "algorithmic_bytes": nbytes, "max_abs_error": err}
 
 
 def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra):
