@@ -9,6 +9,8 @@ benchmark workloads.  Tolerances: the north-star gate (max abs error
 tolerance applies.
 """
 
+import random
+
 import pytest
 import torch
 
@@ -363,3 +365,37 @@ def test_c2_decode_b8_with_scatter_bf16():
     expected = oracle([a.cpu() if isinstance(a, torch.Tensor) else a for a in args])
     assert max_err(actual, expected) <= GATE[torch.bfloat16]
     torch.testing.assert_close(actual.float().cpu(), expected, atol=0.004, rtol=0.015)
+
+
+def random_decode_shape(case):
+    """A seeded random decode shape: head dim, GQA group, batch, block size
+    and ragged lengths (half the cases with one sequence at the maximum)."""
+    rng = random.Random(1000 + case)
+    dim = rng.choice([16, 32, 64, 80, 96, 128, 128, 192, 256])
+    kv = rng.choice([1, 2, 4, 8])
+    heads = kv * rng.choice([1, 2, 3, 4, 8])
+    batch = rng.choice([1, 2, 3, 5, 8, 13, 16, 24, 40, 64])
+    block = rng.choice([1, 7, 16, 32, 64, 256])
+    high = rng.choice([100, 700, 2049, 4096, 5000, 9000])
+    if block == 1:
+        high = min(high, 700)
+    lengths = tuple(rng.randint(1, high) for _ in range(batch))
+    if rng.random() < 0.5:
+        lengths = (high,) + lengths[1:]
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    return dim, heads, kv, block, lengths, dtype
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_random_shapes_every_mode_matches_oracle(case):
+    """The library's plan, the forced balanced walk and forced split-K on the
+    same seeded random shape, each against the oracle."""
+    dim, heads, kv, block, lengths, dtype = random_decode_shape(case)
+    args = decode_inputs(dtype, head_dim=dim, block_size=block, lengths=lengths, heads=heads, kv_heads=kv,
+                         seed=case)
+    dev = to_dev(args)
+    print(f"random decode {case}: D={dim} {heads}/{kv} B={len(lengths)} block={block} max={max(lengths)} {dtype}",
+          flush=True)
+    expected = oracle(args)
+    for partition in (0, -1, 256):
+        assert max_err(paged_attention(*dev, backend="hip", partition_tokens=partition), expected) <= GATE[dtype]
