@@ -8,6 +8,8 @@ fp32 oracle (max abs 2e-3 fp16, 1.6e-2 bf16) and within the reference's own
 tolerance (test_ragged_kernels.py:120).
 """
 
+import random
+
 import pytest
 import torch
 
@@ -430,3 +432,43 @@ def test_trusted_mode_offsets_out_of_order_stay_in_bounds(block):
                                       backend="hip", validate=False)
         torch.cuda.synchronize()
         assert out.shape == q.shape
+
+
+def random_prefill_case(case):
+    """A seeded random ragged prefill: head dim (MFMA tile shapes, narrow and
+    wide rows, the generic kernel), GQA group, page size, sequences with 0 to
+    300 new tokens after 0 to 3000 cached ones, and the key-chunk request."""
+    rng = random.Random(5000 + case)
+    dim = rng.choice([8, 16, 40, 64, 96, 128, 128, 136, 200, 256, 12, 100])
+    kv = rng.choice([1, 2, 4, 8])
+    heads = kv * rng.choice([1, 2, 3, 4, 7, 8])
+    block = rng.choice([5, 16, 64, 256])
+    nseq = rng.choice([1, 2, 3, 6])
+    new = [rng.choice([0, 1, 17, 64, 130, 300]) for _ in range(nseq)]
+    if sum(new) == 0:
+        new[0] = 33
+    priors = [rng.choice([0, 5, 200, 1000, 3000]) for _ in range(nseq)]
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    chunk = rng.choice([0, 0, 256, 512])
+    gen = torch.Generator().manual_seed(case)
+    cu = torch.tensor([0] + torch.tensor(new).cumsum(0).tolist())
+    starts = torch.tensor(priors)
+    lens = starts + torch.tensor(new)
+    width = max(1, -(-int(lens.max()) // block))
+    pages = nseq * width + 3
+    kc = torch.randn(pages, block, kv, dim, generator=gen).to(dtype)
+    vc = torch.randn(pages, block, kv, dim, generator=gen).to(dtype)
+    tables = torch.randperm(pages, generator=gen)[:nseq * width].view(nseq, width)
+    q = torch.randn(int(cu[-1]), heads, dim, generator=gen).to(dtype)
+    return [q, kc, vc, cu, starts, tables, lens], block, chunk, dtype
+
+
+@pytest.mark.parametrize("case", range(16))
+def test_random_prefill_shapes_match_oracle(case):
+    args, block, chunk, dtype = random_prefill_case(case)
+    print(f"random prefill {case}: D={args[0].shape[2]} {args[0].shape[1]}/{args[1].shape[2]} "
+          f"new={(args[3][1:] - args[3][:-1]).tolist()} priors={args[4].tolist()} block={block} chunk={chunk} "
+          f"{dtype}", flush=True)
+    actual = paged_prefill_attention(*[a.to(DEV) for a in args], block, backend="hip", chunk_tokens=chunk)
+    assert torch.isfinite(actual).all()
+    assert max_err(actual, paged_oracle.paged_prefill_attention(*args, block, cast=False)) <= GATE[dtype]
