@@ -205,18 +205,19 @@ int decode_tile_tokens(int64_t head_dim) {
 constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 
 // Host-side plan (lengths stay on the device, so it depends on the table
-// capacity only).  Enough (sequence, kv head) units to occupy every CU, a
-// capacity of one 16-wave step, or two steps with more than a quarter of the
-// CUs' worth of units: one work-group per unit over the whole context, merged
-// in LDS (8 waves; with two work-groups per CU holding every unit, long
-// sequences paired with short ones; below two 16-wave steps, 4 waves when
-// the units outnumber the CUs), or, for one round of long units
-// (kLongUnitBytes), the balanced walk.  (A "16-wave step" is 16 wave
-// iterations of tokens, the unit the thresholds were measured in.)
-// Otherwise split-K into partitions of 4-wave work-groups, sized to give
-// every CU about two work-groups (at least one 4-wave step each), plus a
-// merge kernel.  `requested` > 0 forces split-K with that partition length
-// (rounded to the wave tiling), -1 the balanced walk.
+// capacity only).  Long units (kLongUnitBytes of K+V capacity) numbering at
+// most one per CU take the balanced walk.  Otherwise, enough (sequence, kv
+// head) units to occupy every CU, a capacity of one 16-wave step, or two
+// steps with more than a quarter of the CUs' worth of units: one work-group
+// per unit over the whole context, merged in LDS (8 waves; with two
+// work-groups per CU holding every unit, long sequences paired with short
+// ones; below two 16-wave steps, 4 waves when the units outnumber the CUs).
+// (A "16-wave step" is 16 wave iterations of tokens, the unit the
+// thresholds were measured in.)  Otherwise split-K into partitions of 4-wave
+// work-groups, sized to give every CU about two work-groups (at least one
+// 4-wave step each), plus a merge kernel.  `requested` > 0 forces split-K
+// with that partition length (rounded to the wave tiling), -1 the balanced
+// walk (batch <= 256).
 //
 // Measured at head_dim 128 (bf16, block 16, 16/8 heads, µs per call in a
 // graph): whole-sequence against split-K at 64/128/256 keys.
