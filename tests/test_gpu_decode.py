@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from gpu_cases import decode_inputs
-from mini_engine_hip.kernels.paged import paged_attention
+from mini_engine_hip.kernels.paged import paged_attention, workspace_bytes
 from oracle import c_oracle, paged_oracle
 
 pytestmark = pytest.mark.gpu
@@ -399,3 +399,28 @@ def test_random_shapes_every_mode_matches_oracle(case):
     expected = oracle(args)
     for partition in (0, -1, 256):
         assert max_err(paged_attention(*dev, backend="hip", partition_tokens=partition), expected) <= GATE[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_graph_replay_of_the_balanced_walk_with_new_lengths(dtype):
+    """The plan's balanced walk (long units, fewer than the CUs) captured once
+    and replayed with new context lengths: every replay rewrites the shares'
+    partial rows and merge descriptors from the lengths it finds."""
+    lengths = [5000, 4097, 1, 3000, 700, 4500]
+    args = decode_inputs(dtype, block_size=16, lengths=tuple(lengths), seed=88)
+    dev = to_dev(args)
+    ws = torch.empty(workspace_bytes(len(lengths), 16, 8, 128, 16, dev[3].shape[1]), dtype=torch.uint8, device=DEV)
+    out = torch.empty_like(dev[0])
+    paged_attention(*dev, backend="hip", validate=False, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_attention(*dev, backend="hip", validate=False, out=out, workspace=ws)
+    for replay in range(3):
+        dev[4].copy_(torch.tensor(lengths[replay + 1:] + lengths[:replay + 1], device=DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"walk graph replay {replay} {dtype}", flush=True)
+        expected = oracle([x.cpu() if isinstance(x, torch.Tensor) else x for x in dev])
+        assert max_err(out, expected) <= GATE[dtype]
+        assert torch.equal(out, paged_attention(*dev, backend="hip", validate=False, partition_tokens=-1))
