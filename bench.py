@@ -381,8 +381,8 @@ class CpuLeg:
 # Other workloads of the path (reported under "extra").
 # ---------------------------------------------------------------------------
 
-EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "prefill", "prefill_shapes", "dense_prefill", "kv_scatter",
-               "norm_rope", "after_attention")
+EXTRA_NAMES = ("decode_b1", "decode_b8", "ragged_b64", "decode_shards", "prefill", "prefill_shapes", "dense_prefill",
+               "kv_scatter", "norm_rope", "after_attention")
 
 
 def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_attention, workloads, cpu,
@@ -395,6 +395,8 @@ def extra_workloads(torch, paged_attention, write_kv_cache_slots, paged_prefill_
         _extra_b8(torch, paged_attention, write_kv_cache_slots, workloads, cpu, dev, extra)
     if "ragged_b64" in names:
         _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra)
+    if "decode_shards" in names:
+        _extra_shards(torch, paged_attention, cpu, dev, extra)
     if "prefill" in names:
         _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra)
         _extra_prefill_cold(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra)
@@ -545,6 +547,47 @@ def _extra_ragged(torch, paged_attention, workloads, cpu, dev, extra):
         "us_per_call": walk_call * 1e6, "GBps": nbytes / walk_call / 1e9,
         "frac_of_hbm_peak": nbytes / walk_call / 1e9 / HBM_PEAK_GBS, "split_k_2048_us_per_call": split_call * 1e6,
         "rows": rows, "algorithmic_bytes": nbytes, "max_abs_error": err}
+
+
+def _extra_shards(torch, paged_attention, cpu, dev, extra):
+    """One GPU's share of the headline step under the sharding the path would
+    use (nothing here runs a second GPU): kv heads split over 2 or 8 GPUs (4
+    or 1 kv heads per GPU, with their query heads) or the sequences over 8
+    GPUs (4 per GPU).  Each share runs over 28 separately allocated pools in
+    one graph, as the headline step; layer 0 is checked against the oracle."""
+    shards = {"tp2_kv_heads4": (BATCH, HQ // 2, HKV // 2), "tp8_kv_heads1": (BATCH, HQ // 8, HKV // 8),
+              "dp8_batch4": (BATCH // 8, HQ, HKV)}
+    gen = torch.Generator(device=dev).manual_seed(BASE_SEED + 300)
+    width = CONTEXT // BLOCK
+    result = {}
+    for name, (batch, hq, hkv) in shards.items():
+        pages = batch * width + 7
+        layers = []
+        for _ in range(LAYERS):
+            layers.append({
+                "query": torch.randn((batch, hq, D), generator=gen, device=dev).half(),
+                "key_cache": torch.randn((pages, BLOCK, hkv, D), generator=gen, device=dev).half(),
+                "value_cache": torch.randn((pages, BLOCK, hkv, D), generator=gen, device=dev).half(),
+                "block_tables": torch.randperm(pages, generator=gen, device=dev)[:batch * width].view(batch, width)
+                .contiguous(),
+                "context_lens": torch.full((batch,), CONTEXT, dtype=torch.int64, device=dev)})
+            layers[-1]["out"] = torch.empty_like(layers[-1]["query"])
+
+        def step():
+            for c in layers:
+                paged_attention(*(c[k] for k in DECODE_NAMES), BLOCK, backend="hip", validate=False, out=c["out"])
+        ms, _ = graph_time_ms(step, torch, calls_per_graph=LAYERS, replays=20, warmup=3)
+        per_call = ms / LAYERS * 1e-3
+        nbytes = batch * CONTEXT * hkv * D * 2 * 2 + 2 * batch * hq * D * 2 + batch * width * 8 + batch * 8
+        err = None
+        if cpu is not None:
+            c = layers[0]
+            err = max_abs(c["out"], cpu.decode({k: c[k].cpu() for k in DECODE_NAMES}, BLOCK))
+        result[name] = {"batch": batch, "q_heads": hq, "kv_heads": hkv, "us_per_call": per_call * 1e6,
+                        "GBps": nbytes / per_call / 1e9, "frac_of_hbm_peak": nbytes / per_call / 1e9 / HBM_PEAK_GBS,
+                        "algorithmic_bytes": nbytes, "max_abs_error": err}
+        del layers
+    extra["decode_shards_b32_ctx2048_fp16_28layers"] = result
 
 
 def _extra_prefill(torch, write_kv_cache_slots, paged_prefill_attention, workloads, cpu, dev, extra):
