@@ -146,6 +146,7 @@ def ragged_lengths(batch, high, seed):
     (16, 32, 8, ragged_lengths(9, 5000, 3), 64, False),    # head dim 16: 128-token chunks
     (128, 16, 8, ragged_lengths(16, 8192, 4), 16, True),   # the plan's pick: 128 long units
     (128, 2, 1, (20000,), 16, True),                       # one unit over every share: 256 pieces
+    (128, 2, 1, ragged_lengths(256, 5000, 5), 16, True),   # the plan's pick: 256 sequences, one kv head
 ])
 def test_balanced_walk_matches_oracle(dtype, dim, heads, kv_heads, lengths, block_size, plan):
     """Balanced walk: units laid end to end and cut into equal shares per
