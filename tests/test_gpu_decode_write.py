@@ -12,6 +12,8 @@ whole-sequence and split-K modes, longest-first order, GQA tiles, head dims
 and dtypes, and the attention must match the fp32 oracle.
 """
 
+import random
+
 import pytest
 import torch
 
@@ -108,7 +110,7 @@ def check_equal(step, block, rope, partition_tokens=0, oracle=True):
 @pytest.mark.parametrize("rope", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_headline_shape_whole_sequence(rope, dtype):
-    """B32, Hq16/Hkv8/D128, block 256, ragged lengths up to 2048: one 16-wave
+    """B32, Hq16/Hkv8/D128, block 256, ragged lengths up to 2048: one 8-wave
     work-group per (sequence, kv head), longest sequences first."""
     gen = torch.Generator().manual_seed(3)
     lengths = torch.randint(1, 2049, (32,), generator=gen).tolist()
@@ -223,3 +225,27 @@ def test_in_place_rotation_takes_two_launches():
     with pytest.raises(ValueError, match="overlap"):
         paged_attention_decode_write(raw, step["kc"].clone(), step["vc"].clone(), step["tables"], step["lens"], 16,
                                      step["k"], step["v"], q_out=shifted, **step["norm"])
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_steps_every_mode(case):
+    """Seeded random decode steps (head dim, GQA group, batch, page size,
+    ragged lengths, with or without the norm/RoPE prologue), each through the
+    library's plan, the forced balanced walk and forced split-K: bit-equal to
+    the two launches and within the oracle's gate."""
+    rng = random.Random(7000 + case)
+    head_dim = rng.choice([16, 32, 64, 128, 128, 256])
+    kv_heads = rng.choice([1, 2, 4, 8])
+    q_heads = kv_heads * rng.choice([1, 2, 4, 8])
+    batch = rng.choice([1, 3, 8, 16, 40])
+    block = rng.choice([16, 32, 256])
+    high = rng.choice([300, 2049, 5000])
+    lengths = [rng.randint(1, high) for _ in range(batch)]
+    lengths[0] = high
+    dtype = rng.choice([torch.float16, torch.bfloat16])
+    rope = rng.random() < 0.5
+    step = make_step(batch, q_heads, kv_heads, head_dim, block, lengths, dtype, seed=case)
+    print(f"decode write random {case}: D={head_dim} {q_heads}/{kv_heads} B={batch} block={block} max={high} "
+          f"rope={rope} {dtype}", flush=True)
+    for partition_tokens in (0, -1, 256):
+        check_equal(step, block, rope, partition_tokens=partition_tokens)
