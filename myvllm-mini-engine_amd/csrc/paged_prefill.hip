@@ -937,8 +937,9 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         // biased first unless every key is present and visible to every row
         // of the wave.  p = 2^sc; the exact step (row maxima, rescale of what
         // is accumulated, new probabilities) runs when a row sees its first
-        // key or some probability exceeds 2^8 (inf and NaN included: as bit
-        // patterns of non-negative floats they order above 256).  `first`:
+        // key or some probability, rounded to the operand type, exceeds 2^8
+        // (inf and NaN included: as 16-bit patterns of non-negative values
+        // they order above 256; one packed unsigned max covers two).  `first`:
         // the item's first tile, where nothing is accumulated yet (every
         // rescale factor is 1, so the rescale is skipped).
         auto softmax_tile = [&](int tile, int st, bool first) __attribute__((always_inline)) {
@@ -970,16 +971,20 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
 #pragma unroll
                 for (int nb = 0; nb < SH::kNb; ++nb) {
                     float p[8];
-                    uint32_t top = 0;
 #pragma unroll
                     for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            p[4 * kk + j] = fast_exp2(sc[h][nb][kk][j]);
-                            top = max(top, __float_as_uint(p[4 * kk + j]));
-                        }
-                    need = need | (top > __float_as_uint(kPSumLimit));
+                        for (int j = 0; j < 4; ++j) p[4 * kk + j] = fast_exp2(sc[h][nb][kk][j]);
                     pops[h][nb] = u32x4{T::pack(p[0], p[1]), T::pack(p[2], p[3]), T::pack(p[4], p[5]), T::pack(p[6], p[7])};
+                    {
+                        typedef unsigned short us2 __attribute__((ext_vector_type(2)));
+                        us2 m = __builtin_elementwise_max(__builtin_bit_cast(us2, pops[h][nb][0]),
+                                                          __builtin_bit_cast(us2, pops[h][nb][1]));
+                        m = __builtin_elementwise_max(m, __builtin_bit_cast(us2, pops[h][nb][2]));
+                        m = __builtin_elementwise_max(m, __builtin_bit_cast(us2, pops[h][nb][3]));
+                        const uint32_t lim = T::pack(kPSumLimit, 0.f) & 0xffffu;
+                        need = need | ((uint32_t)max(m.x, m.y) > lim);
+                    }
                 }
             if (__builtin_amdgcn_ballot_w64(need)) {
 #pragma unroll
