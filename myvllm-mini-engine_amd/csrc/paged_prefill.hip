@@ -939,7 +939,8 @@ __device__ __attribute__((always_inline)) void prefill_item(const PrefillArgs& a
         // is accumulated, new probabilities) runs when a row sees its first
         // key or some probability, rounded to the operand type, exceeds 2^8
         // (inf and NaN included: as 16-bit patterns of non-negative values
-        // they order above 256; one packed unsigned max covers two).  `first`:
+        // they order above 256, so an unsigned maximum of the packed halves
+        // decides).  `first`:
         // the item's first tile, where nothing is accumulated yet (every
         // rescale factor is 1, so the rescale is skipped).
         auto softmax_tile = [&](int tile, int st, bool first) __attribute__((always_inline)) {
